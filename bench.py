@@ -1,0 +1,202 @@
+"""Benchmark: full PBC radius-graph rebuild (SFC reorder + cell-list sort + count + write)
+of the 1M-atom, r_cut = 6 A uniform box (config C3) on one MI355X.
+
+    python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu]
+
+One step = one full rebuild through the C ABI (dg_graph_count + dg_graph_write) into
+preallocated output buffers, positions already resident in HBM, no host sync inside the
+step.  Prints ONE JSON line.  `roofline` is for the dominant kernel (the edge-write search
+pass, search_kernel<true>, the only kernel dg_graph_write launches), timed with HIP events
+on the stream it runs on.  `cpu_baseline` times the CPU oracle (a restatement of the
+reference algorithm) on the same box on this host.
+"""
+from __future__ import annotations
+
+import argparse
+import ctypes
+import json
+import os
+import sys
+import time
+
+ROOT = os.path.dirname(os.path.abspath(__file__))
+sys.path.insert(0, ROOT)
+
+HBM_PEAK_GBS = 8000.0
+WRITE_BYTES_PER_EDGE = 28   # edge_index int64 x2 + cell shift fp32 x3
+METRIC = "Gedges/s and ms per full rebuild, 1M atoms r_cut=6 Å, 1 GPU; % HBM peak"
+
+
+def main():
+    ap = argparse.ArgumentParser()
+    ap.add_argument("--gpus", type=int, default=1)
+    ap.add_argument("--steps", type=int, default=20)
+    ap.add_argument("--warmup", type=int, default=5)
+    ap.add_argument("--config", default="C3")
+    ap.add_argument("--no-cpu", action="store_true")
+    ap.add_argument("--cpu-threads", type=int, default=0)
+    args = ap.parse_args()
+    if args.gpus != 1:
+        print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
+              "graph build shards by space with no collective inside it -- see DESIGN.md.",
+              file=sys.stderr)
+        sys.exit(2)
+
+    import numpy as np
+    import torch
+
+    from dynamis_amd import _lib as L
+    from dynamis_amd import configs
+
+    box = {"C1": configs.fcc, "C2": configs.c2, "C3": configs.c3, "C4": configs.c4,
+           "C5": configs.c5}[args.config]()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = L.lib()
+    pos = torch.from_numpy(box.pos).to(dev)
+    tgt = None if box.targets is None else torch.from_numpy(box.targets).to(dev)
+    n = pos.shape[0]
+
+    d = L.GraphDesc()
+    d.n_atoms = n
+    d.has_targets = 0 if tgt is None else 1
+    d.n_targets = 0 if tgt is None else tgt.shape[0]
+    d.pos_dtype = L.DG_F64 if pos.dtype == torch.float64 else L.DG_F32
+    for k, v in enumerate(np.asarray(box.cell, np.float64).reshape(-1)):
+        d.cell[k] = float(v)
+    for k in range(3):
+        d.pbc[k] = 1 if box.pbc[k] else 0
+    d.radius = float(box.radius)
+    nt = n if tgt is None else tgt.shape[0]
+
+    wsb = lib.dg_graph_workspace_size(d)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    counts = torch.empty(nt, dtype=torch.int32, device=dev)
+    s = L.stream_of(dev)
+    stream = torch.cuda.current_stream(dev)
+
+    # size the preallocated edge buffers once (5 % headroom)
+    L.check(lib.dg_graph_count(d, L.ptr(pos), L.ptr(tgt), L.ptr(ws), wsb, L.ptr(counts), s), "count")
+    E0 = L._i64(0)
+    fl = L._i64(0)
+    L.check(lib.dg_graph_read_totals(d, L.ptr(ws), E0, fl, s), "totals")
+    cap = int(E0.value * 1.05) + 1024
+    src = torch.empty(cap, dtype=torch.int64, device=dev)
+    dst = torch.empty(cap, dtype=torch.int64, device=dev)
+    shift = torch.empty((cap, 3), dtype=torch.float32, device=dev)
+
+    def step(ev=None):
+        L.check(lib.dg_graph_count(d, L.ptr(pos), L.ptr(tgt), L.ptr(ws), wsb, L.ptr(counts), s), "count")
+        if ev is not None:
+            ev[0].record(stream)
+        L.check(lib.dg_graph_write(d, L.ptr(pos), L.ptr(tgt), L.ptr(ws), wsb, cap, L.ptr(src), L.ptr(dst),
+                                   L.ptr(shift), None, None, 0, s), "write")
+        if ev is not None:
+            ev[1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
+           for _ in range(args.steps)]
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    torch.cuda.synchronize()
+    t0.record(stream)
+    for k in range(args.steps):
+        step(kev[k])
+    t1.record(stream)
+    torch.cuda.synchronize()
+    total_ms = t0.elapsed_time(t1)
+    write_ms = float(np.mean([a.elapsed_time(b) for a, b in kev]))
+    E = L._i64(0)
+    L.check(lib.dg_graph_read_totals(d, L.ptr(ws), E, fl, s), "totals")
+    E = int(E.value)
+    ms = total_ms / args.steps
+
+    # drop-in Python API (exact-size outputs, one host sync per build)
+    from dynamis_amd.dynamis_state import dynamis_state_impl as impl
+
+    cell_t = torch.from_numpy(np.asarray(box.cell))
+    pbc_t = torch.tensor(list(box.pbc))
+    for _ in range(2):
+        impl.radius_graph_pbc_ex(pos, cell_t, pbc_t, box.radius, 0, False, tgt)
+    torch.cuda.synchronize()
+    ta = time.perf_counter()
+    api_steps = max(3, args.steps // 4)
+    for _ in range(api_steps):
+        impl.radius_graph_pbc_ex(pos, cell_t, pbc_t, box.radius, 0, False, tgt)
+    torch.cuda.synchronize()
+    api_ms = (time.perf_counter() - ta) * 1e3 / api_steps
+
+    pos_bytes = 24 if pos.dtype == torch.float64 else 12
+    # full-rebuild algorithmic bytes: read positions, keys write+read, sorted cell list
+    # write+read, edge outputs
+    rebuild_bytes = pos_bytes * n + 16 * n + 40 * n + WRITE_BYTES_PER_EDGE * E
+    # write kernel algorithmic bytes per launch: edge outputs + one read of the sorted cell
+    # list (16 B position/id + 4 B floor) + per-target counts
+    kbytes = WRITE_BYTES_PER_EDGE * E + 20 * n + 4 * nt
+    achieved = kbytes / (write_ms * 1e-3) / 1e9
+
+    traffic = None
+    tfile = os.path.join(ROOT, "profiles", f"search_write_{args.config}_traffic.json")
+    if os.path.exists(tfile):
+        try:
+            traffic = json.load(open(tfile)).get("bytes_per_launch")
+        except Exception:
+            traffic = None
+
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        thr = args.cpu_threads or min(16, os.cpu_count() or 1)
+        pos_np = box.pos
+        tc = time.perf_counter()
+        o = oracle.radius_graph(pos_np, box.cell, box.pbc, box.radius, target_indices=box.targets,
+                                threads=thr)
+        cpu_s = time.perf_counter() - tc
+        cpu = {"value": round(len(o["src"]) / cpu_s / 1e9, 5), "unit": "Gedges/s", "cores": thr,
+               "kind": "port",
+               "sample": f"one full build of {args.config} ({n} atoms, {len(o['src'])} edges) by the "
+                         f"C oracle (reference algorithm, fp64 predicate), OpenMP {thr} threads, "
+                         f"{cpu_s * 1e3:.0f} ms",
+               "ms_per_rebuild": round(cpu_s * 1e3, 1)}
+        if len(o["src"]) != E:
+            cpu["edge_count_mismatch"] = [len(o["src"]), E]
+        del o
+
+    out = {
+        "metric": METRIC,
+        "value": round(E / (ms * 1e-3) / 1e9, 3),
+        "unit": "Gedges/s",
+        "n_gpus": 1,
+        "steps": args.steps,
+        "warmup": args.warmup,
+        "ms_per_step": round(ms, 4),
+        "higher_is_better": True,
+        "scaling": "weak",
+        "vs_baseline": None,
+        "dtype": "fp32 positions, fp64 predicate, int64 edges",
+        "data": "synthetic (seeded numpy uniform box)",
+        "config": {"workload": f"{args.config}: {box.name} N={n} r_cut={box.radius} "
+                               f"pbc={list(box.pbc)}", "atoms": n, "edges": E,
+                   "parallelism": "single GPU"},
+        "rebuilds_per_s": round(1e3 / ms, 2),
+        "hbm_frac_rebuild": round(rebuild_bytes / (ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+        "count_ms": round(ms - write_ms, 4),
+        "write_ms": round(write_ms, 4),
+        "api_ms_per_rebuild": round(api_ms, 3),
+        "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
+                     "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
+                     "kernel": "search_kernel<true> (edge write)",
+                     "algorithmic_bytes": kbytes},
+        "cpu_baseline": cpu,
+    }
+    if pos.dtype == torch.float64:
+        out["dtype"] = "fp64 positions, fp64 predicate, int64 edges"
+    print(json.dumps(out), flush=True)
+
+
+if __name__ == "__main__":
+    main()

@@ -1,0 +1,1003 @@
+// dg_graph.hip -- PBC radius-graph build for gfx950 (MI355X), C ABI in
+// include/dynamis_graph.h.
+//
+// Pipeline of one build (all on the caller's stream, one host sync in the Python layer
+// to size the outputs, none inside this file):
+//   1. tile_flags / tile_fill      Morton (SFC) rank of every 4x4x4 tile of bins
+//   2. bin_atoms                   fractional coords -> floor (wrap), bin, SFC key, and
+//                                  an atomic slot inside the key's bin
+//   3. scan                        bin starts (counting sort == single-digit radix sort)
+//   4. scatter_atoms               atom id -> sorted slot
+//   5. finish_bins                 stable order inside each bin, then the SoA cell list
+//                                  (fp32 position relative to the bin origin + id,
+//                                  packed floor) in SFC order
+//   6. search<false>               per-target degree (one workgroup per tile, region of
+//                                  (T+2P)^3 bins staged in LDS, one lane per target)
+//   7. scan                        per-tile edge offsets in SFC tile order
+//   8. search<true>                edges: lanes stage (src, shift) records in LDS, the
+//                                  workgroup then streams them out with coalesced stores
+//
+// Reference stages replaced (dynamis_state/src/csrc/graph/radius_graph_kernels.cu):
+// wrap :596-605, selective images :18-141 (here: periodic bin wrap, no image atoms),
+// grid + sort :146-194,662-714, target sort :731-769, count :197-258, write :320-442,
+// outputs :925-933.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <stdio.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/dynamis_graph.h"
+#include "dg_common.hpp"
+#include "dg_plan.hpp"
+#include "dg_scan.hpp"
+
+namespace dg {
+
+thread_local std::string g_last_error;
+
+dg_status fail(dg_status st, const std::string& msg)
+{
+    g_last_error = msg;
+    return st;
+}
+
+constexpr int kCap = 1536;    // region entries staged in LDS per chunk
+constexpr int kStage = 2560;  // edge records staged in LDS per batch (write pass)
+constexpr int kBinSortMax = 128;
+
+__device__ __forceinline__ void load_pos(const void* pos, int f64, int64_t i, double* p)
+{
+    if (f64) {
+        const double* q = (const double*)pos + 3 * i;
+        p[0] = q[0]; p[1] = q[1]; p[2] = q[2];
+    } else {
+        const float* q = (const float*)pos + 3 * i;
+        p[0] = q[0]; p[1] = q[1]; p[2] = q[2];
+    }
+}
+
+struct GridArgs {
+    double C[9], Cinv[9];
+    int nb[3], T[3], ntl[3], mb[3];
+    int tb;
+};
+
+// ---------------------------------------------------------------- tile SFC ranks
+__global__ void tile_flags_kernel(GridArgs g, int64_t ncodes, int* __restrict__ flag)
+{
+    int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= ncodes) return;
+    int x, y, z;
+    morton_decode((uint32_t)c, g.mb, &x, &y, &z);
+    flag[c] = (x < g.ntl[0] && y < g.ntl[1] && z < g.ntl[2]) ? 1 : 0;
+}
+
+__global__ void tile_fill_kernel(GridArgs g, int64_t ncodes, const int* __restrict__ flag,
+                                 const int* __restrict__ cpos, int* __restrict__ tile_of_rank,
+                                 int* __restrict__ rank_of_tile)
+{
+    int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (c >= ncodes || !flag[c]) return;
+    int x, y, z;
+    morton_decode((uint32_t)c, g.mb, &x, &y, &z);
+    int lin = x + g.ntl[0] * (y + g.ntl[1] * z);
+    int r = cpos[c];
+    tile_of_rank[r] = lin;
+    rank_of_tile[lin] = r;
+}
+
+// ---------------------------------------------------------------- binning
+// Canonical wrap of one atom: floor of the fractional coordinate (all axes, as the
+// reference, radius_graph_kernels.cu:603-605), wrapped fraction s in [0,1) and bin b.
+__device__ __forceinline__ int wrap_atom(const GridArgs& g, const double* p, int* f, double* s,
+                                         int* b)
+{
+    int st = 0;
+    double q[3] = {p[0], p[1], p[2]};
+    if (!(isfinite(q[0]) && isfinite(q[1]) && isfinite(q[2]))) {
+        st |= kStatusNonFinite;
+        q[0] = q[1] = q[2] = 0.0;
+    }
+#pragma unroll
+    for (int j = 0; j < 3; ++j) {
+        double fr = canon_frac(q[0], q[1], q[2], g.Cinv, j);
+        double fl = floor(fr);
+        if (!(fabs(fl) <= (double)kFloorMax)) {
+            st |= kStatusRange;
+            fl = 0.0;
+            fr = 0.0;
+        }
+        f[j] = (int)fl;
+        s[j] = fr - fl;
+        int bj = (int)(s[j] * (double)g.nb[j]);
+        b[j] = bj < 0 ? 0 : (bj >= g.nb[j] ? g.nb[j] - 1 : bj);
+    }
+    return st;
+}
+
+__device__ __forceinline__ uint32_t bin_key(const GridArgs& g, const int* b,
+                                            const int* __restrict__ rank_of_tile)
+{
+    int t0 = b[0] / g.T[0], t1 = b[1] / g.T[1], t2 = b[2] / g.T[2];
+    int l0 = b[0] - t0 * g.T[0], l1 = b[1] - t1 * g.T[1], l2 = b[2] - t2 * g.T[2];
+    int lin = t0 + g.ntl[0] * (t1 + g.ntl[1] * t2);
+    return (uint32_t)rank_of_tile[lin] * (uint32_t)g.tb + (uint32_t)(l0 + g.T[0] * (l1 + g.T[1] * l2));
+}
+
+__global__ void bin_atoms_kernel(GridArgs g, const void* __restrict__ pos, int f64, int64_t n,
+                                 const int* __restrict__ rank_of_tile, uint32_t* __restrict__ key,
+                                 uint32_t* __restrict__ rank, int* __restrict__ bcnt,
+                                 int64_t* __restrict__ totals)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    double p[3], s[3];
+    int f[3], b[3];
+    load_pos(pos, f64, i, p);
+    int st = wrap_atom(g, p, f, s, b);
+    if (st) atomicOr((unsigned long long*)&totals[1], (unsigned long long)st);
+    uint32_t k = bin_key(g, b, rank_of_tile);
+    key[i] = k;
+    rank[i] = (uint32_t)atomicAdd(&bcnt[k], 1);
+}
+
+__global__ void scatter_atoms_kernel(int64_t n, const uint32_t* __restrict__ key,
+                                     const uint32_t* __restrict__ rank,
+                                     const int* __restrict__ bstart, int* __restrict__ sid)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    sid[bstart[key[i]] + rank[i]] = (int)i;
+}
+
+// Insertion sort of a[lo, hi) ascending (bins hold a handful of entries).
+__device__ __forceinline__ void small_sort(int* a, int lo, int hi)
+{
+    for (int j = lo + 1; j < hi; ++j) {
+        int v = a[j];
+        int k = j - 1;
+        while (k >= lo && a[k] > v) {
+            a[k + 1] = a[k];
+            --k;
+        }
+        a[k + 1] = v;
+    }
+}
+
+// One thread per bin: stable (by atom id) order inside the bin, then the SoA cell list.
+// Bins with more than kBinSortMax atoms keep the atomic arrival order (edge set and
+// counts are unaffected; only the order of edges within a target can then vary).
+__global__ void finish_bins_kernel(GridArgs g, const void* __restrict__ pos, int f64,
+                                   int64_t nbins, const int* __restrict__ bstart,
+                                   int* __restrict__ sid, float4* __restrict__ spos,
+                                   uint32_t* __restrict__ sflr, int* __restrict__ inv)
+{
+    int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= nbins) return;
+    int lo = bstart[q], hi = bstart[q + 1];
+    if (hi - lo > 1 && hi - lo <= kBinSortMax) small_sort(sid, lo, hi);
+    for (int j = lo; j < hi; ++j) {
+        int i = sid[j];
+        double p[3], s[3];
+        int f[3], b[3];
+        load_pos(pos, f64, i, p);
+        wrap_atom(g, p, f, s, b);
+        // position relative to the bin origin: (s - b/nb) . C
+        double o[3];
+#pragma unroll
+        for (int d = 0; d < 3; ++d) o[d] = s[d] - (double)b[d] / (double)g.nb[d];
+        float4 e;
+        e.x = (float)fma(o[2], g.C[6], fma(o[1], g.C[3], o[0] * g.C[0]));
+        e.y = (float)fma(o[2], g.C[7], fma(o[1], g.C[4], o[0] * g.C[1]));
+        e.z = (float)fma(o[2], g.C[8], fma(o[1], g.C[5], o[0] * g.C[2]));
+        e.w = __int_as_float(i);
+        spos[j] = e;
+        sflr[j] = pack3(f[0], f[1], f[2]);
+        if (inv) inv[i] = j;
+    }
+}
+
+// ---------------------------------------------------------------- explicit targets
+__global__ void bin_targets_kernel(int64_t nt, int64_t n, const int64_t* __restrict__ tgt,
+                                   const uint32_t* __restrict__ key, uint32_t* __restrict__ tkey,
+                                   uint32_t* __restrict__ trank, int* __restrict__ tbcnt,
+                                   int64_t* __restrict__ totals)
+{
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nt) return;
+    int64_t a = tgt[t];
+    if (a < 0 || a >= n) {
+        atomicOr((unsigned long long*)&totals[1], (unsigned long long)DG_FLAG_TARGET);
+        a = 0;
+    }
+    uint32_t k = key[a];
+    tkey[t] = k;
+    trank[t] = (uint32_t)atomicAdd(&tbcnt[k], 1);
+}
+
+__global__ void scatter_targets_kernel(int64_t nt, const uint32_t* __restrict__ tkey,
+                                       const uint32_t* __restrict__ trank,
+                                       const int* __restrict__ tbstart, int* __restrict__ tslot)
+{
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= nt) return;
+    tslot[tbstart[tkey[t]] + trank[t]] = (int)t;
+}
+
+__global__ void finish_targets_kernel(int64_t nbins, int64_t n, const int* __restrict__ tbstart,
+                                      int* __restrict__ tslot, const int64_t* __restrict__ tgt,
+                                      const int* __restrict__ inv, int* __restrict__ tsidx)
+{
+    int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (q >= nbins) return;
+    int lo = tbstart[q], hi = tbstart[q + 1];
+    if (hi - lo > 1 && hi - lo <= kBinSortMax) small_sort(tslot, lo, hi);
+    for (int j = lo; j < hi; ++j) {
+        int64_t a = tgt[tslot[j]];
+        if (a < 0 || a >= n) a = 0;
+        tsidx[j] = inv[a];
+    }
+}
+
+// ---------------------------------------------------------------- neighbour search
+struct SearchArgs {
+    double C[9];
+    double r2;
+    int nb[3], P[3], T[3], ntl[3], R[3], pbc[3];
+    int tb, nregion;
+    int64_t ntiles;
+    float hi, lo_in, tiny;
+    const float4* spos;
+    const uint32_t* sflr;
+    const int* bstart;
+    const int* tile_of_rank;
+    const int* rank_of_tile;
+    const void* pos;
+    int f64;
+    // explicit targets (subset != 0)
+    int subset;
+    const int* tbstart;
+    const int* tsidx;
+    const int* tslot;  // caller position of each sorted target
+    // count pass
+    int* cnt;          // per target, processing order
+    int* counts_user;  // per target, caller order (nullable)
+    int* ttot;         // per tile (rank order)
+    // write pass
+    const int64_t* tbase;
+    int64_t* out_src;
+    int64_t* out_dst;
+    float* out_shift;
+    void* out_vec;
+    void* out_dist;
+    int vout_f64;
+    int64_t capacity;
+    int64_t* totals;
+};
+
+// blockIdx -> tile rank: consecutive workgroups go round-robin to the 8 XCDs, so give
+// each XCD one contiguous range of the Morton order (its own compact region of space,
+// so the halo bins a tile shares with its neighbours hit the same L2).
+__device__ __forceinline__ int64_t xcd_tile_rank(int64_t b, int64_t ntiles)
+{
+    const int64_t q = ntiles >> 3, rem = ntiles & 7;
+    const int64_t x = b & 7, j = b >> 3;
+    return x * q + (x < rem ? x : rem) + j;
+}
+
+struct SearchShared {
+    float4 q[kCap];
+    uint32_t T[kCap];
+    int rp[kMaxRegion + 1];
+    int rg[kMaxRegion];
+    int tbs[65];
+    int boff[kBlock + 1];
+    int tid[kBlock];
+    uint32_t tf[kBlock];
+    int64_t w64[kBlock / 64];
+    int w32[kBlock / 64];
+    int misc[4];
+};
+
+__device__ __forceinline__ void region_offset(const SearchArgs& a, int rx, int ry, int rz,
+                                              float* o)
+{
+    double u0 = (double)(rx - a.P[0]) / (double)a.nb[0];
+    double u1 = (double)(ry - a.P[1]) / (double)a.nb[1];
+    double u2 = (double)(rz - a.P[2]) / (double)a.nb[2];
+#pragma unroll
+    for (int c = 0; c < 3; ++c) o[c] = (float)fma(u2, a.C[6 + c], fma(u1, a.C[3 + c], u0 * a.C[c]));
+}
+
+// Exact (canonical fp64) decision for a candidate the fp32 prefilter cannot settle.
+__device__ __noinline__ bool exact_edge(const SearchArgs& a, int src, int tgt, int S0, int S1,
+                                        int S2)
+{
+    if (src == tgt && S0 == 0 && S1 == 0 && S2 == 0) return false;
+    double ps[3], pt[3], v[3];
+    load_pos(a.pos, a.f64, src, ps);
+    load_pos(a.pos, a.f64, tgt, pt);
+    double d2 = canon_d2(ps, pt, S0, S1, S2, a.C, v);
+    return d2 > kSelfThr && d2 <= a.r2;
+}
+
+template <bool WRITE>
+__global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
+{
+    __shared__ SearchShared sh;
+    __shared__ int2 s_stage[WRITE ? kStage : 1];
+
+    const int64_t rank = xcd_tile_rank(blockIdx.x, a.ntiles);
+    const int lin = a.tile_of_rank[rank];
+    const int tx = lin % a.ntl[0];
+    const int ty = (lin / a.ntl[0]) % a.ntl[1];
+    const int tz = lin / (a.ntl[0] * a.ntl[1]);
+    const int g0[3] = {tx * a.T[0], ty * a.T[1], tz * a.T[2]};
+    const int* tstart = a.subset ? a.tbstart : a.bstart;
+    const int64_t kb = rank * a.tb;
+    const int tbeg = tstart[kb], tend = tstart[kb + a.tb];
+    const int ntg = tend - tbeg;
+    if (ntg == 0) {
+        if (!WRITE && threadIdx.x == 0) a.ttot[rank] = 0;
+        return;
+    }
+    for (int k = threadIdx.x; k <= a.tb; k += kBlock) sh.tbs[k] = tstart[kb + k];
+
+    // ---- region table: (T+2P)^3 bins around the tile, periodic wrap on pbc axes
+    const int R0 = a.R[0], R1 = a.R[1];
+    int c_lo = 0, c_hi = 0, st_lo = 0, st_hi = 0;
+    {
+        const int rb0 = 2 * threadIdx.x, rb1 = rb0 + 1;
+        int cnt2[2] = {0, 0}, st2[2] = {0, 0};
+#pragma unroll
+        for (int h = 0; h < 2; ++h) {
+            int rb = rb0 + h;
+            if (rb >= a.nregion) continue;
+            int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+            int w[3];
+            bool ok = true;
+#pragma unroll
+            for (int d = 0; d < 3; ++d) {
+                int gg = g0[d] - a.P[d] + r[d];
+                if (a.pbc[d]) {
+                    int m = gg % a.nb[d];
+                    w[d] = m < 0 ? m + a.nb[d] : m;
+                } else {
+                    ok = ok && gg >= 0 && gg < a.nb[d];
+                    w[d] = gg;
+                }
+            }
+            if (ok) {
+                int t0 = w[0] / a.T[0], t1 = w[1] / a.T[1], t2 = w[2] / a.T[2];
+                int l0 = w[0] - t0 * a.T[0], l1 = w[1] - t1 * a.T[1], l2 = w[2] - t2 * a.T[2];
+                int tl = t0 + a.ntl[0] * (t1 + a.ntl[1] * t2);
+                int64_t key = (int64_t)a.rank_of_tile[tl] * a.tb + (l0 + a.T[0] * (l1 + a.T[1] * l2));
+                st2[h] = a.bstart[key];
+                cnt2[h] = a.bstart[key + 1] - st2[h];
+            }
+        }
+        c_lo = cnt2[0]; c_hi = cnt2[1]; st_lo = st2[0]; st_hi = st2[1];
+        (void)rb1;
+    }
+    int total;
+    {
+        int ex = block_excl_scan<int, kBlock>(c_lo + c_hi, sh.w32, &total);
+        const int rb0 = 2 * threadIdx.x;
+        if (rb0 < a.nregion) { sh.rp[rb0] = ex; sh.rg[rb0] = st_lo; }
+        if (rb0 + 1 < a.nregion) { sh.rp[rb0 + 1] = ex + c_lo; sh.rg[rb0 + 1] = st_hi; }
+        if (threadIdx.x == 0) sh.rp[a.nregion] = total;
+    }
+    __syncthreads();
+
+    const int nchunks = (total + kCap - 1) / kCap;
+    int loaded = -1;  // chunk currently in LDS
+
+    auto load_chunk = [&](int c) {
+        const int c0 = c * kCap;
+        const int c1 = min(total, c0 + kCap);
+        for (int v = threadIdx.x; v < c1 - c0; v += kBlock) {
+            const int vv = c0 + v;
+            int lo = 0, hi = a.nregion;
+            while (hi - lo > 1) {
+                int mid = (lo + hi) >> 1;
+                if (sh.rp[mid] <= vv) lo = mid; else hi = mid;
+            }
+            const int rb = lo;
+            const int gidx = sh.rg[rb] + (vv - sh.rp[rb]);
+            float4 e = a.spos[gidx];
+            uint32_t fl = a.sflr[gidx];
+            int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+            float o[3];
+            region_offset(a, r[0], r[1], r[2], o);
+            int sb[3];
+#pragma unroll
+            for (int d = 0; d < 3; ++d) {
+                int gg = g0[d] - a.P[d] + r[d];
+                sb[d] = a.pbc[d] ? floor_div(gg, a.nb[d]) : 0;
+            }
+            sh.q[v] = make_float4(e.x + o[0], e.y + o[1], e.z + o[2], e.w);
+            sh.T[v] = pack3(sb[0] - unpack3(fl, 0), sb[1] - unpack3(fl, 1), sb[2] - unpack3(fl, 2));
+        }
+    };
+
+    int64_t tile_edges = 0;            // count pass: tile total
+    int64_t ebase = WRITE ? a.tbase[rank] : 0;
+    bool skip_tile = false;
+    if (WRITE) {
+        int64_t tot_tile = a.tbase[rank + 1] - a.tbase[rank];
+        if (ebase + tot_tile > a.capacity) {
+            skip_tile = true;
+            if (threadIdx.x == 0)
+                atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
+        }
+    }
+    if (skip_tile) return;
+
+    for (int k0 = 0; k0 < ntg; ) {
+        // ---- choose the batch of targets handled by this pass over the region
+        const int kk = k0 + threadIdx.x;
+        int mycnt = 0;
+        if (WRITE && kk < ntg) mycnt = a.cnt[tbeg + kk];
+        int nbatch, ex = 0, btot = 0;
+        bool direct = false;
+        if (WRITE) {
+            ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
+            // targets whose staged records still fit
+            int fits = (kk < ntg && ex + mycnt <= kStage) ? 1 : 0;
+            int nf;
+            block_excl_scan<int, kBlock>(fits, sh.w32, &nf);
+            nbatch = nf;
+            if (nbatch == 0) { nbatch = 1; direct = true; }
+            if (threadIdx.x < nbatch) sh.boff[threadIdx.x] = ex;
+            if (threadIdx.x == nbatch - 1) sh.boff[nbatch] = ex + mycnt;
+            __syncthreads();
+        } else {
+            nbatch = min(kBlock, ntg - k0);
+        }
+        const bool active = threadIdx.x < nbatch;
+
+        // ---- per-lane target state
+        int lx = 0, ly = 0, lz = 0, my_id = 0, caller = 0;
+        uint32_t my_f = 0;
+        float t0 = 0.f, t1 = 0.f, t2 = 0.f;
+        int my_slot = 0;
+        if (active) {
+            const int j = tbeg + kk;
+            int lo = 0, hi = a.tb;
+            while (hi - lo > 1) {
+                int mid = (lo + hi) >> 1;
+                if (sh.tbs[mid] <= j) lo = mid; else hi = mid;
+            }
+            lx = lo % a.T[0];
+            ly = (lo / a.T[0]) % a.T[1];
+            lz = lo / (a.T[0] * a.T[1]);
+            const int sidx = a.subset ? a.tsidx[j] : j;
+            float4 e = a.spos[sidx];
+            my_f = a.sflr[sidx];
+            my_id = __float_as_int(e.w);
+            caller = a.subset ? a.tslot[j] : my_id;
+            float o[3];
+            region_offset(a, lx + a.P[0], ly + a.P[1], lz + a.P[2], o);
+            t0 = e.x + o[0]; t1 = e.y + o[1]; t2 = e.z + o[2];
+            if (WRITE) {
+                sh.tid[threadIdx.x] = my_id;
+                sh.tf[threadIdx.x] = my_f;
+                my_slot = sh.boff[threadIdx.x];
+            }
+        }
+        const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
+        int found = 0;
+
+        for (int c = 0; c < nchunks; ++c) {
+            if (loaded != c) {
+                __syncthreads();
+                load_chunk(c);
+                __syncthreads();
+                loaded = c;
+            }
+            if (!active) continue;
+            const int c0 = c * kCap;
+            const int c1 = min(total, c0 + kCap);
+            for (int dz = 0; dz <= 2 * a.P[2]; ++dz) {
+                for (int dy = 0; dy <= 2 * a.P[1]; ++dy) {
+                    const int rb = ((lz + dz) * R1 + (ly + dy)) * R0 + lx;
+                    int va = sh.rp[rb], vb = sh.rp[rb + 2 * a.P[0] + 1];
+                    va = max(va, c0) - c0;
+                    vb = min(vb, c1) - c0;
+                    for (int v = va; v < vb; ++v) {
+                        const float4 q = sh.q[v];
+                        const float dx = q.x - t0, dyv = q.y - t1, dzv = q.z - t2;
+                        const float d2 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
+                        if (d2 <= a.hi) {
+                            const uint32_t Tp = sh.T[v];
+                            bool edge;
+                            if (d2 < a.lo_in && d2 > a.tiny) {
+                                edge = true;
+                            } else {
+                                edge = exact_edge(a, __float_as_int(q.w), my_id,
+                                                  unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy,
+                                                  unpack3(Tp, 2) + fz);
+                            }
+                            if (edge) {
+                                // found < mycnt always holds (both passes run this exact
+                                // code); the guard keeps a violation from writing out of range
+                                if (WRITE && found < mycnt) {
+                                    if (!direct) {
+                                        s_stage[my_slot + found] = make_int2(__float_as_int(q.w), (int)Tp);
+                                    } else {
+                                        const int64_t o = ebase + found;
+                                        const int S0 = unpack3(Tp, 0) + fx, S1 = unpack3(Tp, 1) + fy,
+                                                  S2 = unpack3(Tp, 2) + fz;
+                                        const int src = __float_as_int(q.w);
+                                        a.out_src[o] = src;
+                                        a.out_dst[o] = my_id;
+                                        a.out_shift[3 * o] = (float)S0;
+                                        a.out_shift[3 * o + 1] = (float)S1;
+                                        a.out_shift[3 * o + 2] = (float)S2;
+                                        if (a.out_vec || a.out_dist) {
+                                            double ps[3], pt[3], vv[3];
+                                            load_pos(a.pos, a.f64, src, ps);
+                                            load_pos(a.pos, a.f64, my_id, pt);
+                                            double dd = canon_d2(ps, pt, S0, S1, S2, a.C, vv);
+                                            if (a.vout_f64) {
+                                                if (a.out_vec) {
+                                                    double* ov = (double*)a.out_vec + 3 * o;
+                                                    ov[0] = vv[0]; ov[1] = vv[1]; ov[2] = vv[2];
+                                                }
+                                                if (a.out_dist) ((double*)a.out_dist)[o] = sqrt(dd);
+                                            } else {
+                                                if (a.out_vec) {
+                                                    float* ov = (float*)a.out_vec + 3 * o;
+                                                    ov[0] = (float)vv[0]; ov[1] = (float)vv[1]; ov[2] = (float)vv[2];
+                                                }
+                                                if (a.out_dist) ((float*)a.out_dist)[o] = (float)sqrt(dd);
+                                            }
+                                        }
+                                    }
+                                }
+                                ++found;
+                            }
+                        }
+                    }
+                }
+            }
+        }
+
+        if (!WRITE) {
+            if (active) {
+                a.cnt[tbeg + kk] = found;
+                if (a.counts_user) a.counts_user[caller] = found;
+            }
+            int64_t bt;
+            block_excl_scan<int64_t, kBlock>((int64_t)found, sh.w64, &bt);
+            tile_edges += bt;
+            k0 += nbatch;
+            continue;
+        }
+
+        // ---- write pass: stream the staged records out, fully coalesced
+        __syncthreads();
+        if (!direct) {
+            const int nE = sh.boff[nbatch];
+            for (int e = threadIdx.x; e < nE; e += kBlock) {
+                int lo = 0, hi = nbatch;
+                while (hi - lo > 1) {
+                    int mid = (lo + hi) >> 1;
+                    if (sh.boff[mid] <= e) lo = mid; else hi = mid;
+                }
+                const int2 rec = s_stage[e];
+                const uint32_t ft = sh.tf[lo];
+                const int dst = sh.tid[lo];
+                const int S0 = unpack3((uint32_t)rec.y, 0) + unpack3(ft, 0);
+                const int S1 = unpack3((uint32_t)rec.y, 1) + unpack3(ft, 1);
+                const int S2 = unpack3((uint32_t)rec.y, 2) + unpack3(ft, 2);
+                const int64_t o = ebase + e;
+                a.out_src[o] = rec.x;
+                a.out_dst[o] = dst;
+                a.out_shift[3 * o] = (float)S0;
+                a.out_shift[3 * o + 1] = (float)S1;
+                a.out_shift[3 * o + 2] = (float)S2;
+                if (a.out_vec || a.out_dist) {
+                    double ps[3], pt[3], vv[3];
+                    load_pos(a.pos, a.f64, rec.x, ps);
+                    load_pos(a.pos, a.f64, dst, pt);
+                    double dd = canon_d2(ps, pt, S0, S1, S2, a.C, vv);
+                    if (a.vout_f64) {
+                        if (a.out_vec) {
+                            double* ov = (double*)a.out_vec + 3 * o;
+                            ov[0] = vv[0]; ov[1] = vv[1]; ov[2] = vv[2];
+                        }
+                        if (a.out_dist) ((double*)a.out_dist)[o] = sqrt(dd);
+                    } else {
+                        if (a.out_vec) {
+                            float* ov = (float*)a.out_vec + 3 * o;
+                            ov[0] = (float)vv[0]; ov[1] = (float)vv[1]; ov[2] = (float)vv[2];
+                        }
+                        if (a.out_dist) ((float*)a.out_dist)[o] = (float)sqrt(dd);
+                    }
+                }
+            }
+            ebase += nE;
+        } else {
+            ebase += a.cnt[tbeg + k0];
+        }
+        __syncthreads();
+        k0 += nbatch;
+    }
+    if (!WRITE && threadIdx.x == 0) a.ttot[rank] = (int)tile_edges;
+}
+
+// ---------------------------------------------------------------- all-pairs fallback
+// Used only when the search region of a tile would exceed kMaxRegion bins (cutoff much
+// larger than the cell).  One thread per target, every atom, every periodic image in
+// |S_d| <= ceil(cutoff_frac_d) + 1.
+struct BruteArgs {
+    double C[9], Cinv[9];
+    double r2;
+    int pbc[3], kimg[3];
+    const void* pos;
+    int f64;
+    int64_t n, nt;
+    const int64_t* tgt;
+    int* cnt;
+    int* counts_user;
+    const int64_t* offs;
+    int64_t* out_src;
+    int64_t* out_dst;
+    float* out_shift;
+    void* out_vec;
+    void* out_dist;
+    int vout_f64;
+    int64_t capacity;
+    int64_t* totals;
+};
+
+__device__ __forceinline__ void brute_floor(const BruteArgs& a, const double* p, int* f)
+{
+#pragma unroll
+    for (int j = 0; j < 3; ++j) f[j] = (int)floor(canon_frac(p[0], p[1], p[2], a.Cinv, j));
+}
+
+template <bool WRITE>
+__global__ void brute_kernel(BruteArgs a)
+{
+    int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (t >= a.nt) return;
+    int64_t tg = a.tgt ? a.tgt[t] : t;
+    if (tg < 0 || tg >= a.n) {
+        atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)DG_FLAG_TARGET);
+        if (!WRITE) { a.cnt[t] = 0; if (a.counts_user) a.counts_user[t] = 0; }
+        return;
+    }
+    double pt[3];
+    int ft[3];
+    load_pos(a.pos, a.f64, tg, pt);
+    brute_floor(a, pt, ft);
+    int64_t o = WRITE ? a.offs[t] : 0;
+    if (WRITE && a.offs[t + 1] > a.capacity) {
+        atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
+        return;
+    }
+    int found = 0;
+    for (int64_t j = 0; j < a.n; ++j) {
+        double ps[3];
+        int fs[3];
+        load_pos(a.pos, a.f64, j, ps);
+        brute_floor(a, ps, fs);
+        int lo[3], hi[3];
+        for (int d = 0; d < 3; ++d) {
+            if (a.pbc[d]) { lo[d] = -a.kimg[d]; hi[d] = a.kimg[d]; }
+            else { lo[d] = hi[d] = ft[d] - fs[d]; }
+        }
+        for (int s0 = lo[0]; s0 <= hi[0]; ++s0)
+            for (int s1 = lo[1]; s1 <= hi[1]; ++s1)
+                for (int s2 = lo[2]; s2 <= hi[2]; ++s2) {
+                    double v[3];
+                    double d2 = canon_d2(ps, pt, s0, s1, s2, a.C, v);
+                    if (!(d2 > kSelfThr && d2 <= a.r2)) continue;
+                    if (WRITE) {
+                        int64_t e = o + found;
+                        a.out_src[e] = j;
+                        a.out_dst[e] = tg;
+                        a.out_shift[3 * e] = (float)s0;
+                        a.out_shift[3 * e + 1] = (float)s1;
+                        a.out_shift[3 * e + 2] = (float)s2;
+                        if (a.out_vec) {
+                            if (a.vout_f64) {
+                                double* ov = (double*)a.out_vec + 3 * e;
+                                ov[0] = v[0]; ov[1] = v[1]; ov[2] = v[2];
+                            } else {
+                                float* ov = (float*)a.out_vec + 3 * e;
+                                ov[0] = (float)v[0]; ov[1] = (float)v[1]; ov[2] = (float)v[2];
+                            }
+                        }
+                        if (a.out_dist) {
+                            if (a.vout_f64) ((double*)a.out_dist)[e] = sqrt(d2);
+                            else ((float*)a.out_dist)[e] = (float)sqrt(d2);
+                        }
+                    }
+                    ++found;
+                }
+    }
+    if (!WRITE) {
+        a.cnt[t] = found;
+        if (a.counts_user) a.counts_user[t] = found;
+    }
+}
+
+// ---------------------------------------------------------------- small utilities
+__global__ void zero_i32_kernel(int* __restrict__ p, int64_t n)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+__global__ void zero_i64_kernel(int64_t* __restrict__ p, int64_t n)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) p[i] = 0;
+}
+
+__global__ void copy_total_kernel(const int64_t* __restrict__ src, int64_t* __restrict__ totals)
+{
+    if (threadIdx.x == 0 && blockIdx.x == 0) totals[0] = src[0];
+}
+
+inline unsigned nblocks(int64_t n, int b = 256) { return (unsigned)((n + b - 1) / b); }
+
+template <typename T>
+inline T* at(void* ws, size_t off)
+{
+    return (T*)((char*)ws + off);
+}
+
+dg_status check_launch(const char* what)
+{
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess)
+        return fail(DG_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+    return DG_OK;
+}
+
+// Validates the description and builds the plan (host only).
+dg_status make_plan(const dg_graph_desc* d, Plan& p)
+{
+    if (!d) return fail(DG_ERR_INVALID, "desc is NULL");
+    if (d->n_atoms < 0 || d->n_atoms > 0x7ffffff0LL)
+        return fail(DG_ERR_INVALID, "n_atoms must be in [0, 2^31)");
+    if (d->has_targets && (d->n_targets < 0 || d->n_targets > 0x7ffffff0LL))
+        return fail(DG_ERR_INVALID, "n_targets must be in [0, 2^31)");
+    if (d->pos_dtype != DG_F32 && d->pos_dtype != DG_F64)
+        return fail(DG_ERR_INVALID, "pos must be float32 or float64");
+    if (!(d->radius > 0.0) || !isfinite(d->radius))
+        return fail(DG_ERR_INVALID, "radius must be positive, got " + std::to_string(d->radius));
+    for (int k = 0; k < 9; ++k)
+        if (!isfinite(d->cell[k])) return fail(DG_ERR_INVALID, "cell must be finite");
+    p = Plan();
+    p.n = d->n_atoms;
+    p.subset = d->has_targets ? 1 : 0;
+    p.nt = d->has_targets ? d->n_targets : d->n_atoms;
+    p.f64 = d->pos_dtype == DG_F64;
+    if (plan_geometry(p, d->cell, d->pbc, d->radius)) return fail(DG_ERR_INVALID, "cell is singular");
+    plan_grid(p);
+    plan_layout(p);
+    if (p.nbins >= 0x7fffffffLL || p.ncodes >= 0x7fffffffLL)
+        return fail(DG_ERR_INVALID, "grid too large");
+    return DG_OK;
+}
+
+GridArgs grid_args(const Plan& p)
+{
+    GridArgs g;
+    memcpy(g.C, p.C, sizeof g.C);
+    memcpy(g.Cinv, p.Cinv, sizeof g.Cinv);
+    for (int d = 0; d < 3; ++d) {
+        g.nb[d] = p.nb[d]; g.T[d] = p.T[d]; g.ntl[d] = p.ntl[d]; g.mb[d] = p.mb[d];
+    }
+    g.tb = p.tb;
+    return g;
+}
+
+SearchArgs search_args(const Plan& p, const void* pos, void* ws)
+{
+    SearchArgs a;
+    memset(&a, 0, sizeof a);
+    memcpy(a.C, p.C, sizeof a.C);
+    a.r2 = p.r2;
+    for (int d = 0; d < 3; ++d) {
+        a.nb[d] = p.nb[d]; a.P[d] = p.P[d]; a.T[d] = p.T[d]; a.ntl[d] = p.ntl[d];
+        a.R[d] = p.R[d]; a.pbc[d] = p.pbc[d];
+    }
+    a.tb = p.tb;
+    a.nregion = p.nregion;
+    a.ntiles = p.ntiles;
+    a.hi = p.hi; a.lo_in = p.lo_in; a.tiny = p.tiny;
+    a.spos = at<float4>(ws, p.o_spos);
+    a.sflr = at<uint32_t>(ws, p.o_sflr);
+    a.bstart = at<int>(ws, p.o_bstart);
+    a.tile_of_rank = at<int>(ws, p.o_tor);
+    a.rank_of_tile = at<int>(ws, p.o_rot);
+    a.pos = pos;
+    a.f64 = p.f64;
+    a.subset = p.subset;
+    a.tbstart = at<int>(ws, p.o_tbstart);
+    a.tsidx = at<int>(ws, p.o_tsidx);
+    a.tslot = at<int>(ws, p.o_tslot);
+    a.cnt = at<int>(ws, p.o_cnt);
+    a.ttot = at<int>(ws, p.o_ttot);
+    a.tbase = at<int64_t>(ws, p.o_tbase);
+    a.totals = at<int64_t>(ws, p.o_tot);
+    return a;
+}
+
+BruteArgs brute_args(const Plan& p, const void* pos, const int64_t* tgt, void* ws)
+{
+    BruteArgs b;
+    memset(&b, 0, sizeof b);
+    memcpy(b.C, p.C, sizeof b.C);
+    memcpy(b.Cinv, p.Cinv, sizeof b.Cinv);
+    b.r2 = p.r2;
+    for (int d = 0; d < 3; ++d) { b.pbc[d] = p.pbc[d]; b.kimg[d] = p.kimg[d]; }
+    b.pos = pos;
+    b.f64 = p.f64;
+    b.n = p.n;
+    b.nt = p.nt;
+    b.tgt = p.subset ? tgt : nullptr;
+    b.cnt = at<int>(ws, p.o_cnt);
+    b.offs = at<int64_t>(ws, p.o_tbase);
+    b.totals = at<int64_t>(ws, p.o_tot);
+    return b;
+}
+
+}  // namespace dg
+
+using namespace dg;
+
+extern "C" {
+
+const char* dg_last_error(void) { return g_last_error.c_str(); }
+
+const char* dg_version(void) { return "dynamis_graph 0.1 gfx950"; }
+
+size_t dg_graph_workspace_size(const dg_graph_desc* desc)
+{
+    Plan p;
+    if (make_plan(desc, p) != DG_OK) return 0;
+    return p.ws_bytes;
+}
+
+dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                         void* ws, size_t ws_bytes, int32_t* counts_out, hipStream_t s)
+{
+    Plan p;
+    dg_status st = make_plan(desc, p);
+    if (st != DG_OK) return st;
+    if (!ws || ws_bytes < p.ws_bytes) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    if (p.n > 0 && !pos) return fail(DG_ERR_INVALID, "pos is NULL");
+    if (p.subset && p.nt > 0 && !target_idx) return fail(DG_ERR_INVALID, "target_idx is NULL");
+    g_last_error.clear();
+    int64_t* totals = at<int64_t>(ws, p.o_tot);
+    hipLaunchKernelGGL(zero_i64_kernel, dim3(1), dim3(64), 0, s, totals, (int64_t)8);
+    if (p.n == 0 || p.nt == 0) {
+        if (counts_out && p.nt > 0)
+            hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nt)), dim3(256), 0, s, counts_out, p.nt);
+        return check_launch("dg_graph_count(empty)");
+    }
+    if (p.brute) {
+        BruteArgs b = brute_args(p, pos, target_idx, ws);
+        b.counts_user = counts_out;
+        hipLaunchKernelGGL(brute_kernel<false>, dim3(nblocks(p.nt, 64)), dim3(64), 0, s, b);
+        device_excl_scan<int, int64_t>(at<int>(ws, p.o_cnt), p.nt, at<int64_t>(ws, p.o_tbase),
+                                       at<int64_t>(ws, p.o_part), s);
+        hipLaunchKernelGGL(copy_total_kernel, dim3(1), dim3(64), 0, s,
+                           at<int64_t>(ws, p.o_tbase) + p.nt, totals);
+        return check_launch("dg_graph_count(brute)");
+    }
+    GridArgs g = grid_args(p);
+    // 1. Morton rank of the tiles
+    int* cflag = at<int>(ws, p.o_cflag);
+    int* cpos = at<int>(ws, p.o_cpos);
+    hipLaunchKernelGGL(tile_flags_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes, cflag);
+    device_excl_scan<int, int>(cflag, p.ncodes, cpos, at<int>(ws, p.o_part), s);
+    hipLaunchKernelGGL(tile_fill_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes,
+                       cflag, cpos, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot));
+    // 2-5. counting sort of the atoms into SFC-ordered bins
+    int* bcnt = at<int>(ws, p.o_bcnt);
+    int* bstart = at<int>(ws, p.o_bstart);
+    hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, bcnt, p.nbins);
+    hipLaunchKernelGGL(bin_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, g, pos, p.f64, p.n,
+                       (const int*)at<int>(ws, p.o_rot), at<uint32_t>(ws, p.o_key),
+                       at<uint32_t>(ws, p.o_rank), bcnt, totals);
+    device_excl_scan<int, int>(bcnt, p.nbins, bstart, at<int>(ws, p.o_part), s);
+    hipLaunchKernelGGL(scatter_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, p.n,
+                       (const uint32_t*)at<uint32_t>(ws, p.o_key),
+                       (const uint32_t*)at<uint32_t>(ws, p.o_rank), (const int*)bstart,
+                       at<int>(ws, p.o_sid));
+    hipLaunchKernelGGL(finish_bins_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, g, pos, p.f64,
+                       p.nbins, (const int*)bstart, at<int>(ws, p.o_sid), at<float4>(ws, p.o_spos),
+                       at<uint32_t>(ws, p.o_sflr), p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr);
+    if (p.subset) {
+        int* tbcnt = at<int>(ws, p.o_tbcnt);
+        int* tbstart = at<int>(ws, p.o_tbstart);
+        hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, tbcnt, p.nbins);
+        hipLaunchKernelGGL(bin_targets_kernel, dim3(nblocks(p.nt)), dim3(256), 0, s, p.nt, p.n,
+                           target_idx, (const uint32_t*)at<uint32_t>(ws, p.o_key),
+                           at<uint32_t>(ws, p.o_tkey), at<uint32_t>(ws, p.o_trank), tbcnt, totals);
+        device_excl_scan<int, int>(tbcnt, p.nbins, tbstart, at<int>(ws, p.o_part), s);
+        hipLaunchKernelGGL(scatter_targets_kernel, dim3(nblocks(p.nt)), dim3(256), 0, s, p.nt,
+                           (const uint32_t*)at<uint32_t>(ws, p.o_tkey),
+                           (const uint32_t*)at<uint32_t>(ws, p.o_trank), (const int*)tbstart,
+                           at<int>(ws, p.o_tslot));
+        hipLaunchKernelGGL(finish_targets_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, p.nbins,
+                           p.n, (const int*)tbstart, at<int>(ws, p.o_tslot), target_idx,
+                           (const int*)at<int>(ws, p.o_inv), at<int>(ws, p.o_tsidx));
+    }
+    // 6. degrees
+    SearchArgs a = search_args(p, pos, ws);
+    a.counts_user = counts_out;
+    hipLaunchKernelGGL(search_kernel<false>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    // 7. tile offsets in SFC order
+    device_excl_scan<int, int64_t>(at<int>(ws, p.o_ttot), p.ntiles, at<int64_t>(ws, p.o_tbase),
+                                   at<int64_t>(ws, p.o_part), s);
+    hipLaunchKernelGGL(copy_total_kernel, dim3(1), dim3(64), 0, s,
+                       at<int64_t>(ws, p.o_tbase) + p.ntiles, totals);
+    return check_launch("dg_graph_count");
+}
+
+dg_status dg_graph_read_totals(const dg_graph_desc* desc, const void* ws, int64_t* total_edges,
+                               int64_t* flags, hipStream_t s)
+{
+    Plan p;
+    dg_status st = make_plan(desc, p);
+    if (st != DG_OK) return st;
+    int64_t h[2] = {0, 0};
+    hipError_t e = hipMemcpyAsync(h, at<int64_t>((void*)ws, p.o_tot), sizeof h, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("read totals: ") + hipGetErrorString(e));
+    if (total_edges) *total_edges = h[0];
+    if (flags) *flags = h[1];
+    if (h[1] & (DG_FLAG_RANGE | DG_FLAG_NONFINITE | DG_FLAG_TARGET)) {
+        std::string m;
+        if (h[1] & DG_FLAG_NONFINITE) m += "pos contains non-finite values; ";
+        if (h[1] & DG_FLAG_RANGE) m += "an atom lies more than 255 cell lengths outside the cell; ";
+        if (h[1] & DG_FLAG_TARGET) m += "target_indices out of range [0, N); ";
+        return fail(DG_ERR_RANGE, m);
+    }
+    if (h[1] & DG_FLAG_CAPACITY) return fail(DG_ERR_CAPACITY, "edge capacity exceeded");
+    return DG_OK;
+}
+
+dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                         void* ws, size_t ws_bytes, int64_t capacity, int64_t* edge_src,
+                         int64_t* edge_dst, float* cell_shift, void* edge_vec, void* edge_dist,
+                         int32_t vec_dtype, hipStream_t s)
+{
+    Plan p;
+    dg_status st = make_plan(desc, p);
+    if (st != DG_OK) return st;
+    if (!ws || ws_bytes < p.ws_bytes) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    if (vec_dtype != DG_F32 && vec_dtype != DG_F64) return fail(DG_ERR_INVALID, "vec_dtype");
+    if (capacity < 0) return fail(DG_ERR_INVALID, "capacity < 0");
+    g_last_error.clear();
+    if (p.n == 0 || p.nt == 0 || capacity == 0) return DG_OK;
+    if (!edge_src || !edge_dst || !cell_shift) return fail(DG_ERR_INVALID, "edge outputs are NULL");
+    if (p.brute) {
+        BruteArgs b = brute_args(p, pos, target_idx, ws);
+        b.out_src = edge_src; b.out_dst = edge_dst; b.out_shift = cell_shift;
+        b.out_vec = edge_vec; b.out_dist = edge_dist; b.vout_f64 = vec_dtype == DG_F64;
+        b.capacity = capacity;
+        hipLaunchKernelGGL(brute_kernel<true>, dim3(nblocks(p.nt, 64)), dim3(64), 0, s, b);
+        return check_launch("dg_graph_write(brute)");
+    }
+    SearchArgs a = search_args(p, pos, ws);
+    a.out_src = edge_src; a.out_dst = edge_dst; a.out_shift = cell_shift;
+    a.out_vec = edge_vec; a.out_dist = edge_dist; a.vout_f64 = vec_dtype == DG_F64;
+    a.capacity = capacity;
+    hipLaunchKernelGGL(search_kernel<true>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    return check_launch("dg_graph_write");
+}
+
+}  // extern "C"

@@ -1,0 +1,179 @@
+// dg_plan.hpp -- host-side plan of one radius-graph build: cell geometry, the periodic
+// fractional bin grid, the tile decomposition, the fp32 prefilter band and the layout of
+// the caller-provided device workspace.
+//
+// Geometry follows dynamis_state/src/csrc/graph/radius_graph_kernels.cu:515-594
+// (plane spacings d_face = |V| / |a_j x a_k|, cutoff_frac = r / d_face, cell^-1 by the
+// adjugate), evaluated in fp64.  The grid differs from the reference's Cartesian bounding
+// box (:662-692): bins are laid out in FRACTIONAL coordinates, nb_d bins along lattice
+// vector d, so a triclinic cell is binned without empty corners and periodic images are
+// reached by wrapping the bin index instead of materialising image atoms (:18-141).
+#pragma once
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <algorithm>
+
+namespace dg {
+
+constexpr int kBlock = 256;      // threads per search workgroup (4 x wave64)
+constexpr int kMaxRegion = 512;  // region bins staged per tile
+constexpr int kTileEdge = 4;     // target bins per tile edge (4x4x4)
+
+struct Plan {
+    int64_t n = 0, nt = 0;  // atoms, targets
+    int subset = 0;         // explicit target list
+    int f64 = 0;            // positions are fp64
+    double C[9], Cinv[9];
+    double r = 0, r2 = 0;
+    double d_face[3], cf[3];
+    int pbc[3];
+    int nb[3], P[3], T[3], ntl[3], R[3], mb[3];
+    int tb = 0;             // bins per tile
+    int64_t ntiles = 0, nbins = 0, ncodes = 0;
+    int nregion = 0;
+    int brute = 0;          // region too large: all-pairs path
+    int kimg[3];            // brute path: |S_d| range on periodic axes
+    float hi = 0, lo_in = 0, tiny = 0;
+    // workspace layout (byte offsets)
+    size_t o_key, o_rank, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
+    size_t o_cflag, o_cpos, o_tor, o_rot;
+    size_t o_tkey, o_trank, o_tbcnt, o_tbstart, o_tslot, o_tsidx, o_tcaller;
+    size_t o_cnt, o_ttot, o_tbase, o_part, o_tot;
+    size_t ws_bytes = 0;
+};
+
+inline size_t align_up(size_t x) { return (x + 255) & ~(size_t)255; }
+
+// Fills geometry; returns nonzero for a singular / non-finite cell.
+inline int plan_geometry(Plan& p, const double* cell, const uint8_t* pbc, double r)
+{
+    const double *a0 = cell, *a1 = cell + 3, *a2 = cell + 6;
+    double c12[3] = {a1[1] * a2[2] - a1[2] * a2[1], a1[2] * a2[0] - a1[0] * a2[2],
+                     a1[0] * a2[1] - a1[1] * a2[0]};
+    double c20[3] = {a2[1] * a0[2] - a2[2] * a0[1], a2[2] * a0[0] - a2[0] * a0[2],
+                     a2[0] * a0[1] - a2[1] * a0[0]};
+    double c01[3] = {a0[1] * a1[2] - a0[2] * a1[1], a0[2] * a1[0] - a0[0] * a1[2],
+                     a0[0] * a1[1] - a0[1] * a1[0]};
+    double vol = a0[0] * c12[0] + a0[1] * c12[1] + a0[2] * c12[2];
+    if (!(fabs(vol) > 0.0) || !isfinite(vol)) return 1;
+    memcpy(p.C, cell, sizeof p.C);
+    const double* cs[3] = {c12, c20, c01};
+    double av = fabs(vol);
+    for (int d = 0; d < 3; d++) {
+        double nrm = sqrt(cs[d][0] * cs[d][0] + cs[d][1] * cs[d][1] + cs[d][2] * cs[d][2]);
+        p.d_face[d] = av / nrm;
+        p.cf[d] = r / p.d_face[d];
+        p.pbc[d] = pbc[d] ? 1 : 0;
+    }
+    for (int i = 0; i < 3; i++)
+        for (int j = 0; j < 3; j++) p.Cinv[i * 3 + j] = cs[j][i] / vol;
+    p.r = r;
+    p.r2 = r * r;
+    return 0;
+}
+
+inline void plan_grid(Plan& p)
+{
+    // Bins: thickness >= r/2 between bin planes (cf * nb <= 2), capped so that a sparse
+    // system does not allocate many more bins than atoms.
+    double nbd[3];
+    for (int d = 0; d < 3; d++) {
+        double v = floor(2.0 / p.cf[d] * (1.0 - 1e-6));
+        nbd[d] = std::min(std::max(v, 1.0), 1024.0);
+    }
+    const double cap = std::max(4.0 * (double)p.n, 4096.0);
+    while (nbd[0] * nbd[1] * nbd[2] > cap) {
+        double s = cbrt(nbd[0] * nbd[1] * nbd[2] / cap);
+        if (s < 1.01) s = 1.01;
+        for (int d = 0; d < 3; d++) nbd[d] = std::max(1.0, floor(nbd[d] / s));
+    }
+    for (int d = 0; d < 3; d++) {
+        p.nb[d] = (int)nbd[d];
+        p.P[d] = (int)ceil(p.cf[d] * p.nb[d] * (1.0 + 1e-9) + 1e-12);
+        if (p.P[d] < 1) p.P[d] = 1;
+        p.T[d] = std::min(kTileEdge, p.nb[d]);
+    }
+    auto region = [&]() {
+        return (int64_t)(p.T[0] + 2 * p.P[0]) * (p.T[1] + 2 * p.P[1]) * (p.T[2] + 2 * p.P[2]);
+    };
+    while (region() > kMaxRegion) {
+        int best = -1;
+        for (int d = 0; d < 3; d++)
+            if (p.T[d] > 1 && (best < 0 || p.T[d] + 2 * p.P[d] > p.T[best] + 2 * p.P[best])) best = d;
+        if (best < 0) break;
+        p.T[best]--;
+    }
+    p.brute = region() > kMaxRegion;
+    for (int d = 0; d < 3; d++) {
+        p.R[d] = p.T[d] + 2 * p.P[d];
+        p.ntl[d] = (p.nb[d] + p.T[d] - 1) / p.T[d];
+        int b = 0;
+        while ((1 << b) < p.ntl[d]) b++;
+        p.mb[d] = b;
+        p.kimg[d] = p.pbc[d] ? (int)ceil(p.cf[d]) + 1 : 0;
+    }
+    p.nregion = p.R[0] * p.R[1] * p.R[2];
+    p.tb = p.T[0] * p.T[1] * p.T[2];
+    p.ntiles = (int64_t)p.ntl[0] * p.ntl[1] * p.ntl[2];
+    p.nbins = p.ntiles * p.tb;
+    p.ncodes = (int64_t)1 << (p.mb[0] + p.mb[1] + p.mb[2]);
+
+    // fp32 prefilter band.  Positions in LDS are fp32 offsets from the tile origin:
+    // (position - bin origin) rounded once, plus (bin origin - tile origin) rounded once.
+    // delta bounds the per-component error of the fp32 difference vector.
+    const double u = 1.0 / 16777216.0;  // 2^-24
+    double len[3], bin_diag = 0, reg_diag = 0;
+    for (int d = 0; d < 3; d++) {
+        len[d] = sqrt(p.C[3 * d] * p.C[3 * d] + p.C[3 * d + 1] * p.C[3 * d + 1] +
+                      p.C[3 * d + 2] * p.C[3 * d + 2]);
+        bin_diag += len[d] / p.nb[d];
+        reg_diag += len[d] * (double)p.R[d] / p.nb[d];
+    }
+    double delta = 8.0 * u * (bin_diag + reg_diag + p.r);
+    double rr = p.r + 2.0 * delta;
+    double band = 2.0 * (2.0 * sqrt(3.0) * rr * delta + 3.0 * delta * delta + 4.0 * u * rr * rr);
+    p.hi = nextafterf((float)(p.r2 + band), INFINITY);
+    double lo = p.r2 - band;
+    p.lo_in = lo > 0 ? nextafterf((float)lo, 0.0f) : 0.0f;
+    double t = sqrt(kSelfThr) + 2.0 * sqrt(3.0) * delta;
+    p.tiny = nextafterf((float)(t * t * (1.0 + 1e-3)), INFINITY);
+}
+
+inline void plan_layout(Plan& p)
+{
+    size_t o = 0;
+    auto take = [&](size_t bytes) { size_t r = o; o = align_up(o + (bytes ? bytes : 1)); return r; };
+    const size_t n = (size_t)p.n, nt = (size_t)p.nt, nbins = (size_t)p.nbins;
+    const size_t nc = (size_t)p.ncodes, ntl = (size_t)p.ntiles;
+    p.o_tot = take(8 * 8);
+    p.o_key = take(4 * n);
+    p.o_rank = take(4 * n);
+    p.o_bcnt = take(4 * nbins);
+    p.o_bstart = take(4 * (nbins + 1));
+    p.o_sid = take(4 * n);
+    p.o_spos = take(16 * n);
+    p.o_sflr = take(4 * n);
+    p.o_inv = take(p.subset ? 4 * n : 0);
+    p.o_cflag = take(4 * nc);
+    p.o_cpos = take(4 * (nc + 1));
+    p.o_tor = take(4 * ntl);
+    p.o_rot = take(4 * ntl);
+    p.o_tkey = take(p.subset ? 4 * nt : 0);
+    p.o_trank = take(p.subset ? 4 * nt : 0);
+    p.o_tbcnt = take(p.subset ? 4 * nbins : 0);
+    p.o_tbstart = take(p.subset ? 4 * (nbins + 1) : 0);
+    p.o_tslot = take(p.subset ? 4 * nt : 0);
+    p.o_tsidx = take(p.subset ? 4 * nt : 0);
+    p.o_tcaller = take(p.subset ? 4 * nt : 0);
+    p.o_cnt = take(4 * nt);
+    p.o_ttot = take(4 * std::max(ntl, nt));
+    p.o_tbase = take(8 * (std::max(ntl, nt) + 1));
+    // scan partials: one int64 per 2048-item block of the largest scan
+    size_t big = std::max(std::max(nbins + 1, nc + 1), std::max(ntl, nt) + 1);
+    p.o_part = take(8 * (big / 2048 + 2));
+    p.ws_bytes = o;
+}
+
+}  // namespace dg

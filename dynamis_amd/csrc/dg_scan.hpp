@@ -1,0 +1,118 @@
+// dg_scan.hpp -- wave64 / workgroup / device-wide exclusive scans used by the graph build.
+#pragma once
+#include <hip/hip_runtime.h>
+#include <stdint.h>
+
+namespace dg {
+
+constexpr int kScanBlock = 256;
+constexpr int kScanItems = 8;
+constexpr int kScanTile = kScanBlock * kScanItems;  // 2048 items per workgroup
+
+// Inclusive scan across one wave64.
+template <typename T>
+__device__ __forceinline__ T wave_incl_scan(T x)
+{
+    const int lane = threadIdx.x & 63;
+#pragma unroll
+    for (int o = 1; o < 64; o <<= 1) {
+        T y = __shfl_up(x, o, 64);
+        if (lane >= o) x += y;
+    }
+    return x;
+}
+
+// Exclusive scan across a workgroup of NT threads (NT multiple of 64).  s_w holds
+// NT/64 values.  Returns the exclusive prefix; *total receives the workgroup sum.
+template <typename T, int NT>
+__device__ __forceinline__ T block_excl_scan(T v, T* s_w, T* total)
+{
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    T x = wave_incl_scan(v);
+    if (lane == 63) s_w[w] = x;
+    __syncthreads();
+    T before = 0, tot = 0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) {
+        T s = s_w[i];
+        before += (i < w) ? s : (T)0;
+        tot += s;
+    }
+    __syncthreads();
+    *total = tot;
+    return before + x - v;
+}
+
+// Phase 1: per-workgroup sums of kScanTile items.
+template <typename Tin, typename Tout>
+__global__ __launch_bounds__(kScanBlock) void scan_reduce_kernel(const Tin* __restrict__ in,
+                                                                 int64_t n, Tout* __restrict__ part)
+{
+    __shared__ Tout s_w[kScanBlock / 64];
+    int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+    Tout s = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k)
+        if (base + k < n) s += (Tout)in[base + k];
+    Tout tot;
+    block_excl_scan<Tout, kScanBlock>(s, s_w, &tot);
+    if (threadIdx.x == 0) part[blockIdx.x] = tot;
+}
+
+// Phase 2: one workgroup scans the partials in place (exclusive), any length.
+template <typename Tout>
+__global__ __launch_bounds__(kScanBlock) void scan_partials_kernel(Tout* __restrict__ part,
+                                                                   int64_t nblk)
+{
+    __shared__ Tout s_w[kScanBlock / 64];
+    Tout carry = 0;
+    for (int64_t b0 = 0; b0 < nblk; b0 += kScanBlock) {
+        int64_t i = b0 + threadIdx.x;
+        Tout v = i < nblk ? part[i] : (Tout)0;
+        Tout tot;
+        Tout ex = block_excl_scan<Tout, kScanBlock>(v, s_w, &tot);
+        if (i < nblk) part[i] = carry + ex;
+        carry += tot;
+    }
+}
+
+// Phase 3: exclusive scan of each tile plus its offset; out has n+1 entries, out[n] = sum.
+template <typename Tin, typename Tout>
+__global__ __launch_bounds__(kScanBlock) void scan_final_kernel(const Tin* __restrict__ in,
+                                                                int64_t n,
+                                                                const Tout* __restrict__ part,
+                                                                Tout* __restrict__ out)
+{
+    __shared__ Tout s_w[kScanBlock / 64];
+    int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
+    Tout v[kScanItems];
+    Tout s = 0;
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        v[k] = (base + k < n) ? (Tout)in[base + k] : (Tout)0;
+        s += v[k];
+    }
+    Tout tot;
+    Tout ex = block_excl_scan<Tout, kScanBlock>(s, s_w, &tot) + part[blockIdx.x];
+#pragma unroll
+    for (int k = 0; k < kScanItems; ++k) {
+        if (base + k < n) out[base + k] = ex;
+        ex += v[k];
+    }
+    if (blockIdx.x == gridDim.x - 1 && threadIdx.x == kScanBlock - 1) out[n] = ex;
+}
+
+// Host helper: exclusive scan of in[0..n) into out[0..n] (out[n] = total).
+// part needs n / kScanTile + 1 entries of Tout.
+template <typename Tin, typename Tout>
+inline void device_excl_scan(const Tin* in, int64_t n, Tout* out, Tout* part, hipStream_t s)
+{
+    int64_t nblk = n / kScanTile + 1;
+    hipLaunchKernelGGL((scan_reduce_kernel<Tin, Tout>), dim3((unsigned)nblk), dim3(kScanBlock), 0,
+                       s, in, n, part);
+    hipLaunchKernelGGL((scan_partials_kernel<Tout>), dim3(1), dim3(kScanBlock), 0, s, part, nblk);
+    hipLaunchKernelGGL((scan_final_kernel<Tin, Tout>), dim3((unsigned)nblk), dim3(kScanBlock), 0,
+                       s, in, n, part, out);
+}
+
+}  // namespace dg

@@ -1,0 +1,480 @@
+// dg_sfc.hip -- SFC keys, stable LSD radix sort and partition labels for gfx950, plus the
+// order-preserving edge filter.  C ABI in include/dynamis_graph.h.
+//
+// Keys follow dynamis_state/src/csrc/partition/sfc_kernels.cu:
+//   bounds  :196-198   pos_min = min over atoms, range = max - min (0 -> 1), fp32
+//   Morton  :32-56     21-bit quantisation (p - min) / range * (2^21 - 1), clamp, interleave
+//                      with x at bit 0 (fp32 arithmetic)
+//   Hilbert :62-109    order-7 quantisation with the reference's per-bit transform
+//   labels  :114-173   unweighted closed form / exact int64 weighted cut
+// The sort replaces at::sort (sfc_kernels.cu:224) with a stable 8-bit LSD radix sort whose
+// pass count adapts to the key bits that actually vary.
+#include <hip/hip_runtime.h>
+#include <math.h>
+#include <stdint.h>
+#include <string.h>
+
+#include <string>
+
+#include "../../include/dynamis_graph.h"
+#include "dg_common.hpp"
+#include "dg_scan.hpp"
+
+namespace dg {
+dg_status fail(dg_status st, const std::string& msg);
+}
+
+namespace {
+using namespace dg;
+
+constexpr int kRsBlock = 256;
+constexpr int kRsRounds = 4;
+constexpr int kRsTile = kRsBlock * kRsRounds;  // keys per workgroup per pass
+
+inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
+inline unsigned nblk(int64_t n, int b = 256) { return (unsigned)((n + b - 1) / b); }
+
+// ------------------------------------------------------------------ bounds
+__global__ void bounds_partial_kernel(const float* __restrict__ pos, int64_t n,
+                                      float* __restrict__ part)
+{
+    __shared__ float s_mn[3][256], s_mx[3][256];
+    float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+    for (int64_t i = (int64_t)blockIdx.x * 256 + threadIdx.x; i < n; i += (int64_t)gridDim.x * 256)
+        for (int a = 0; a < 3; ++a) {
+            float v = pos[3 * i + a];
+            mn[a] = fminf(mn[a], v);
+            mx[a] = fmaxf(mx[a], v);
+        }
+    for (int a = 0; a < 3; ++a) { s_mn[a][threadIdx.x] = mn[a]; s_mx[a][threadIdx.x] = mx[a]; }
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if (threadIdx.x < o)
+            for (int a = 0; a < 3; ++a) {
+                s_mn[a][threadIdx.x] = fminf(s_mn[a][threadIdx.x], s_mn[a][threadIdx.x + o]);
+                s_mx[a][threadIdx.x] = fmaxf(s_mx[a][threadIdx.x], s_mx[a][threadIdx.x + o]);
+            }
+        __syncthreads();
+    }
+    if (threadIdx.x == 0)
+        for (int a = 0; a < 3; ++a) {
+            part[6 * blockIdx.x + a] = s_mn[a][0];
+            part[6 * blockIdx.x + 3 + a] = s_mx[a][0];
+        }
+}
+
+__global__ void bounds_final_kernel(const float* __restrict__ part, int nb, float* __restrict__ out)
+{
+    if (threadIdx.x != 0) return;
+    for (int a = 0; a < 3; ++a) {
+        float mn = INFINITY, mx = -INFINITY;
+        for (int b = 0; b < nb; ++b) {
+            mn = fminf(mn, part[6 * b + a]);
+            mx = fmaxf(mx, part[6 * b + 3 + a]);
+        }
+        float rg = mx - mn;
+        out[a] = mn;
+        out[3 + a] = rg > 0.0f ? rg : 1.0f;
+    }
+}
+
+// ------------------------------------------------------------------ keys
+// Spread the low 21 bits of v to every third bit (standard magic-mask bit interleave).
+__device__ __forceinline__ uint64_t spread21(uint32_t v)
+{
+    uint64_t x = v & 0x1fffffu;
+    x = (x | (x << 32)) & 0x001f00000000ffffull;
+    x = (x | (x << 16)) & 0x001f0000ff0000ffull;
+    x = (x | (x << 8)) & 0x100f00f00f00f00full;
+    x = (x | (x << 4)) & 0x10c30c30c30c30c3ull;
+    x = (x | (x << 2)) & 0x1249249249249249ull;
+    return x;
+}
+
+__global__ void keys_kernel(const float* __restrict__ pos, int64_t n, int curve,
+                            const float* __restrict__ bnd, int64_t* __restrict__ keys)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    float u[3];
+    for (int a = 0; a < 3; ++a) u[a] = (pos[3 * i + a] - bnd[a]) / bnd[3 + a];
+    if (curve == 0) {
+        const uint32_t gm = (1u << 21) - 1;
+        uint32_t q[3];
+        for (int a = 0; a < 3; ++a) {
+            uint32_t t = (uint32_t)(u[a] * (float)gm);
+            q[a] = t < gm ? t : gm;
+        }
+        keys[i] = (int64_t)(spread21(q[0]) | (spread21(q[1]) << 1) | (spread21(q[2]) << 2));
+    } else {
+        const int gm = 127;
+        int c[3];
+        for (int a = 0; a < 3; ++a) {
+            int t = (int)(u[a] * (float)gm);
+            c[a] = t < 0 ? 0 : (t > gm ? gm : t);
+        }
+        int64_t r = 0;
+        for (int b = 0; b < 7; ++b) {
+            int xb = (c[0] >> b) & 1, yb = (c[1] >> b) & 1, zb = (c[2] >> b) & 1;
+            int nx = xb, ny = yb, nz = zb;
+            if (b > 0) {
+                // per-bit rule of sfc_kernels.cu:94-101
+                nx = xb ? zb : 0;
+                ny = xb ? yb : (yb ? zb : 0);
+                nz = xb ? yb : (yb ? xb : (zb ? yb : 0));
+            }
+            r |= ((int64_t)nx << (3 * b)) | ((int64_t)ny << (3 * b + 1)) | ((int64_t)nz << (3 * b + 2));
+        }
+        keys[i] = r;
+    }
+}
+
+// ------------------------------------------------------------------ radix sort
+// OR / AND of all keys tell which bytes vary.
+__global__ void key_span_kernel(const int64_t* __restrict__ keys, int64_t n,
+                                unsigned long long* __restrict__ span)
+{
+    unsigned long long o = 0, a = ~0ull;
+    for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
+         i += (int64_t)gridDim.x * blockDim.x) {
+        unsigned long long k = (unsigned long long)keys[i] ^ 0x8000000000000000ull;
+        o |= k;
+        a &= k;
+    }
+    atomicOr(&span[0], o);
+    atomicAnd(&span[1], a);
+}
+
+__global__ void span_init_kernel(unsigned long long* span)
+{
+    if (threadIdx.x == 0) { span[0] = 0; span[1] = ~0ull; }
+}
+
+__device__ __forceinline__ int digit_of(int64_t k, int shift)
+{
+    return (int)((((unsigned long long)k ^ 0x8000000000000000ull) >> shift) & 0xffu);
+}
+
+// Per-workgroup digit histogram, stored digit-major: hist[d * nblocks + b].
+__global__ __launch_bounds__(kRsBlock) void rs_hist_kernel(const int64_t* __restrict__ keys,
+                                                           int64_t n, int shift,
+                                                           int* __restrict__ hist, int nblocks)
+{
+    __shared__ int h[256];
+    h[threadIdx.x] = 0;
+    __syncthreads();
+    int64_t base = (int64_t)blockIdx.x * kRsTile;
+    for (int r = 0; r < kRsRounds; ++r) {
+        int64_t i = base + r * kRsBlock + threadIdx.x;
+        if (i < n) atomicAdd(&h[digit_of(keys[i], shift)], 1);
+    }
+    __syncthreads();
+    hist[threadIdx.x * nblocks + blockIdx.x] = h[threadIdx.x];
+}
+
+// Stable scatter: items are ranked in index order within the workgroup (round by round,
+// wave by wave, lane by lane) using ballot match masks.
+__global__ __launch_bounds__(kRsBlock) void rs_scatter_kernel(
+    const int64_t* __restrict__ kin, const int64_t* __restrict__ vin, int64_t n, int shift,
+    const int* __restrict__ offs, int nblocks, int64_t* __restrict__ kout, int64_t* __restrict__ vout)
+{
+    __shared__ int run[256];
+    __shared__ int wc[kRsBlock / 64][256];
+    const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
+    run[threadIdx.x] = offs[threadIdx.x * nblocks + blockIdx.x];
+    for (int k = 0; k < kRsBlock / 64; ++k) wc[k][threadIdx.x] = 0;
+    __syncthreads();
+    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
+    int64_t base = (int64_t)blockIdx.x * kRsTile;
+    for (int r = 0; r < kRsRounds; ++r) {
+        int64_t i = base + r * kRsBlock + threadIdx.x;
+        const bool valid = i < n;
+        int64_t k = valid ? kin[i] : 0;
+        int64_t v = valid ? (vin ? vin[i] : i) : 0;
+        int d = valid ? digit_of(k, shift) : 0;
+        uint64_t match = __ballot(valid);
+        for (int bit = 0; bit < 8; ++bit) {
+            uint64_t b = __ballot(valid && ((d >> bit) & 1));
+            match &= ((d >> bit) & 1) ? b : ~b;
+        }
+        int inwave = __popcll(match & lt);
+        bool leader = valid && inwave == 0;
+        if (leader) wc[w][d] = __popcll(match);
+        __syncthreads();
+        if (valid) {
+            int pre = run[d];
+            for (int k2 = 0; k2 < w; ++k2) pre += wc[k2][d];
+            int64_t dst = pre + inwave;
+            kout[dst] = k;
+            vout[dst] = v;
+        }
+        __syncthreads();
+        // advance the running offsets and clear the per-wave counts
+        int add = 0;
+        for (int k2 = 0; k2 < kRsBlock / 64; ++k2) {
+            add += wc[k2][threadIdx.x];
+            wc[k2][threadIdx.x] = 0;
+        }
+        run[threadIdx.x] += add;
+        __syncthreads();
+    }
+}
+
+__global__ void iota_kernel(int64_t n, int64_t* __restrict__ out)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = i;
+}
+
+// ------------------------------------------------------------------ labels
+__global__ void labels_unweighted_kernel(const int64_t* __restrict__ perm, int64_t n, int64_t W,
+                                         int64_t* __restrict__ labels)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t p = 0;
+    if (W > 1) {
+        int64_t base = n / W, rem = n % W, thr = rem * (base + 1);
+        p = i < thr ? i / (base + 1) : rem + (i - thr) / (base > 0 ? base : 1);
+        if (p > W - 1) p = W - 1;
+    }
+    labels[perm[i]] = p;
+}
+
+__global__ void gather_weights_kernel(const int64_t* __restrict__ perm, int64_t n,
+                                      const int64_t* __restrict__ w, int64_t* __restrict__ out)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < n) out[i] = w[perm[i]];
+}
+
+// cs_excl[i+1] is the inclusive prefix of the sorted weights at i.
+__global__ void labels_weighted_kernel(const int64_t* __restrict__ perm, int64_t n, int64_t W,
+                                       const int64_t* __restrict__ cs_excl,
+                                       int64_t* __restrict__ labels)
+{
+    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i >= n) return;
+    int64_t total = cs_excl[n];
+    int64_t c = cs_excl[i + 1];
+    int64_t p = total > 0 ? (c * W) / total : 0;
+    if (p < 0) p = 0;
+    if (p > W - 1) p = W - 1;
+    labels[perm[i]] = p;
+}
+
+// ------------------------------------------------------------------ edge filter
+__device__ __forceinline__ double shift_at(const void* sh, int dt, int64_t k)
+{
+    if (dt == DG_F32) return (double)((const float*)sh)[k];
+    if (dt == DG_F64) return ((const double*)sh)[k];
+    return (double)((const int64_t*)sh)[k];
+}
+
+// keep iff canonical d2 <= r^2 (dist_graph_ops_kernels.cu:16-43 keeps d2 <= r2, no lower bound)
+__global__ void filter_flag_kernel(const void* __restrict__ pos, int f64, const double* cellp,
+                                   double r2, const int64_t* __restrict__ src,
+                                   const int64_t* __restrict__ dst, const void* __restrict__ sh,
+                                   int sdt, int64_t E, int* __restrict__ flag, double c0, double c1,
+                                   double c2, double c3, double c4, double c5, double c6, double c7,
+                                   double c8)
+{
+    int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    const double C[9] = {c0, c1, c2, c3, c4, c5, c6, c7, c8};
+    (void)cellp;
+    double ps[3], pt[3];
+    const int64_t s = src[e], d = dst[e];
+    if (f64) {
+        const double* a = (const double*)pos;
+        for (int k = 0; k < 3; ++k) { ps[k] = a[3 * s + k]; pt[k] = a[3 * d + k]; }
+    } else {
+        const float* a = (const float*)pos;
+        for (int k = 0; k < 3; ++k) { ps[k] = a[3 * s + k]; pt[k] = a[3 * d + k]; }
+    }
+    const double S0 = shift_at(sh, sdt, 3 * e), S1 = shift_at(sh, sdt, 3 * e + 1),
+                 S2 = shift_at(sh, sdt, 3 * e + 2);
+    double v[3];
+    for (int a = 0; a < 3; ++a)
+        v[a] = (ps[a] - pt[a]) + fma(S2, C[6 + a], fma(S1, C[3 + a], S0 * C[a]));
+    double d2 = fma(v[2], v[2], fma(v[1], v[1], v[0] * v[0]));
+    flag[e] = d2 <= r2 ? 1 : 0;
+}
+
+__global__ void filter_compact_kernel(const int* __restrict__ flag, const int64_t* __restrict__ pre,
+                                      int64_t E, int64_t* __restrict__ keep_idx,
+                                      int64_t* __restrict__ n_kept)
+{
+    int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e < E && flag[e]) keep_idx[pre[e]] = e;
+    if (e == 0) *n_kept = pre[E];
+}
+
+dg_status launch_ok(const char* what)
+{
+    hipError_t e = hipGetLastError();
+    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string(what) + ": " + hipGetErrorString(e));
+    return DG_OK;
+}
+
+struct SortLayout {
+    size_t o_k0, o_v0, o_k1, o_v1, o_hist, o_offs, o_part, o_span, total;
+    int nblocks;
+};
+
+SortLayout sort_layout(int64_t n)
+{
+    SortLayout L;
+    size_t o = 0;
+    auto take = [&](size_t b) { size_t r = o; o = al(o + (b ? b : 1)); return r; };
+    L.nblocks = (int)((n + kRsTile - 1) / kRsTile);
+    if (L.nblocks < 1) L.nblocks = 1;
+    size_t nh = (size_t)L.nblocks * 256;
+    L.o_k0 = take(8 * n);
+    L.o_v0 = take(8 * n);
+    L.o_k1 = take(8 * n);
+    L.o_v1 = take(8 * n);
+    L.o_hist = take(4 * nh);
+    L.o_offs = take(4 * (nh + 1));
+    L.o_part = take(4 * (nh / kScanTile + 2));
+    L.o_span = take(16);
+    L.total = o;
+    return L;
+}
+
+}  // namespace
+
+extern "C" {
+
+size_t dg_sfc_workspace_size(int64_t n)
+{
+    if (n < 0) return 0;
+    SortLayout L = sort_layout(n);
+    size_t bounds = al(6 * 4 * 1024 + 64);
+    // keys need the bounds scratch; order needs the sort layout; labels need 8*(2n+2)
+    size_t lab = al(8 * (size_t)(n + 1)) * 2 + al(8 * ((size_t)n / kScanTile + 2));
+    size_t m = L.total > bounds ? L.total : bounds;
+    return m > lab ? m : lab;
+}
+
+dg_status dg_sfc_keys(const float* pos, int64_t n, int32_t curve, int64_t* keys, void* ws,
+                      size_t ws_bytes, hipStream_t s)
+{
+    if (n < 0) return fail(DG_ERR_INVALID, "n < 0");
+    if (curve != 0 && curve != 1) return fail(DG_ERR_INVALID, "curve must be 0 (Morton) or 1 (Hilbert)");
+    if (n == 0) return DG_OK;
+    if (ws_bytes < dg_sfc_workspace_size(n)) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    float* part = (float*)ws;
+    float* bnd = part + 6 * 1024;
+    int nb = (int)((n + 255) / 256);
+    if (nb > 1024) nb = 1024;
+    hipLaunchKernelGGL(bounds_partial_kernel, dim3(nb), dim3(256), 0, s, pos, n, part);
+    hipLaunchKernelGGL(bounds_final_kernel, dim3(1), dim3(64), 0, s, (const float*)part, nb, bnd);
+    hipLaunchKernelGGL(keys_kernel, dim3(nblk(n)), dim3(256), 0, s, pos, n, (int)curve,
+                       (const float*)bnd, keys);
+    return launch_ok("dg_sfc_keys");
+}
+
+dg_status dg_sfc_order(const int64_t* keys, int64_t n, int64_t* perm, void* ws, size_t ws_bytes,
+                       hipStream_t s)
+{
+    if (n < 0) return fail(DG_ERR_INVALID, "n < 0");
+    if (n == 0) return DG_OK;
+    if (n > 0x7ffffff0LL) return fail(DG_ERR_INVALID, "n too large");
+    SortLayout L = sort_layout(n);
+    if (ws_bytes < L.total) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    char* w = (char*)ws;
+    unsigned long long* span = (unsigned long long*)(w + L.o_span);
+    hipLaunchKernelGGL(span_init_kernel, dim3(1), dim3(64), 0, s, span);
+    hipLaunchKernelGGL(key_span_kernel, dim3(nblk(n) > 1024 ? 1024 : nblk(n)), dim3(256), 0, s, keys, n, span);
+    unsigned long long h[2];
+    hipError_t e = hipMemcpyAsync(h, span, sizeof h, hipMemcpyDeviceToHost, s);
+    if (e == hipSuccess) e = hipStreamSynchronize(s);
+    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("dg_sfc_order: ") + hipGetErrorString(e));
+    unsigned long long vary = h[0] & ~h[1];
+    const int64_t* kin = keys;
+    const int64_t* vin = nullptr;
+    int64_t* kb[2] = {(int64_t*)(w + L.o_k0), (int64_t*)(w + L.o_k1)};
+    int64_t* vb[2] = {(int64_t*)(w + L.o_v0), (int64_t*)(w + L.o_v1)};
+    int cur = 0;
+    int passes = 0;
+    for (int shift = 0; shift < 64; shift += 8) {
+        if (((vary >> shift) & 0xffull) == 0) continue;
+        int* hist = (int*)(w + L.o_hist);
+        int* offs = (int*)(w + L.o_offs);
+        int64_t nh = (int64_t)L.nblocks * 256;
+        hipLaunchKernelGGL(rs_hist_kernel, dim3(L.nblocks), dim3(kRsBlock), 0, s, kin, n, shift, hist, L.nblocks);
+        device_excl_scan<int, int>(hist, nh, offs, (int*)(w + L.o_part), s);
+        hipLaunchKernelGGL(rs_scatter_kernel, dim3(L.nblocks), dim3(kRsBlock), 0, s, kin, vin, n, shift,
+                           (const int*)offs, L.nblocks, kb[cur], vb[cur]);
+        kin = kb[cur];
+        vin = vb[cur];
+        cur ^= 1;
+        ++passes;
+    }
+    if (passes == 0) {
+        // all keys equal: identity permutation
+        hipLaunchKernelGGL(iota_kernel, dim3(nblk(n)), dim3(256), 0, s, n, perm);
+        return launch_ok("dg_sfc_order");
+    }
+    e = hipMemcpyAsync(perm, vin, 8 * (size_t)n, hipMemcpyDeviceToDevice, s);
+    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("dg_sfc_order: ") + hipGetErrorString(e));
+    return launch_ok("dg_sfc_order");
+}
+
+dg_status dg_sfc_labels(const int64_t* perm, int64_t n, int64_t W, const int64_t* weights,
+                        int64_t* labels, void* ws, size_t ws_bytes, hipStream_t s)
+{
+    if (n < 0 || W < 1) return fail(DG_ERR_INVALID, "need n >= 0 and n_parts >= 1");
+    if (n == 0) return DG_OK;
+    if (ws_bytes < dg_sfc_workspace_size(n)) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    if (!weights || W == 1) {
+        hipLaunchKernelGGL(labels_unweighted_kernel, dim3(nblk(n)), dim3(256), 0, s, perm, n,
+                           weights ? (int64_t)1 : W, labels);
+        return launch_ok("dg_sfc_labels");
+    }
+    char* w = (char*)ws;
+    int64_t* sw = (int64_t*)w;
+    int64_t* cs = (int64_t*)(w + al(8 * (size_t)(n + 1)));
+    int64_t* part = (int64_t*)(w + 2 * al(8 * (size_t)(n + 1)));
+    hipLaunchKernelGGL(gather_weights_kernel, dim3(nblk(n)), dim3(256), 0, s, perm, n, weights, sw);
+    device_excl_scan<int64_t, int64_t>(sw, n, cs, part, s);
+    hipLaunchKernelGGL(labels_weighted_kernel, dim3(nblk(n)), dim3(256), 0, s, perm, n, W,
+                       (const int64_t*)cs, labels);
+    return launch_ok("dg_sfc_labels");
+}
+
+size_t dg_filter_workspace_size(int64_t E)
+{
+    if (E < 0) return 0;
+    return al(4 * (size_t)E) + al(8 * (size_t)(E + 1)) + al(8 * ((size_t)E / kScanTile + 2));
+}
+
+dg_status dg_filter_edges_to_radius(const void* pos, int32_t pos_dtype, int64_t n_atoms,
+                                    const double* cell, double radius, const int64_t* src,
+                                    const int64_t* dst, const void* shift, int32_t shift_dtype,
+                                    int64_t E, int64_t* keep_idx, int64_t* n_kept, void* ws,
+                                    size_t ws_bytes, hipStream_t s)
+{
+    if (pos_dtype != DG_F32 && pos_dtype != DG_F64) return fail(DG_ERR_INVALID, "pos dtype");
+    if (shift_dtype != DG_F32 && shift_dtype != DG_F64 && shift_dtype != 2)
+        return fail(DG_ERR_INVALID, "shift dtype");
+    if (!(radius > 0.0)) return fail(DG_ERR_INVALID, "radius must be positive");
+    if (E < 0 || n_atoms < 0) return fail(DG_ERR_INVALID, "negative size");
+    if (ws_bytes < dg_filter_workspace_size(E)) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    char* w = (char*)ws;
+    int* flag = (int*)w;
+    int64_t* pre = (int64_t*)(w + al(4 * (size_t)E));
+    int64_t* part = (int64_t*)(w + al(4 * (size_t)E) + al(8 * (size_t)(E + 1)));
+    if (E > 0)
+        hipLaunchKernelGGL(filter_flag_kernel, dim3(nblk(E)), dim3(256), 0, s, pos,
+                           (int)(pos_dtype == DG_F64), (const double*)nullptr, radius * radius, src,
+                           dst, shift, (int)shift_dtype, E, flag, cell[0], cell[1], cell[2], cell[3],
+                           cell[4], cell[5], cell[6], cell[7], cell[8]);
+    device_excl_scan<int, int64_t>(flag, E, pre, part, s);
+    hipLaunchKernelGGL(filter_compact_kernel, dim3(E > 0 ? nblk(E) : 1), dim3(256), 0, s,
+                       (const int*)flag, (const int64_t*)pre, E, keep_idx, n_kept);
+    return launch_ok("dg_filter_edges_to_radius");
+}
+
+}  // extern "C"

@@ -1,0 +1,318 @@
+"""MI355X implementation of the ``dynamis_state_impl`` graph entry points.
+
+Same names, arguments, return tensors and error messages as the reference's pybind11
+module (dynamis_state/src/dynamis_state_bindings.cpp:153-163, 241-254; validation in
+dynamis_state/src/csrc/graph/radius_graph.cpp:7-127 and dist_graph_ops.cpp:5-35;
+stubs dynamis_state/src/dynamis_state/dynamis_state_impl.pyi:213-258), running the
+hand-written gfx950 kernels of libdynamis_graph.so.  There is no CPU path: every
+function requires device tensors and the built library.
+
+Differences from the reference, all deliberate:
+  * the cutoff predicate is the fp64 canonical one (see include/dynamis_graph.h), not
+    fp32 -- edge sets agree except for pairs within ~1e-5 A of the cutoff;
+  * ``pos`` may also be float64 (the cell is then used in float64);
+  * edges come grouped by target in space-filling-curve order (the reference groups
+    them by target in cell order); compare edge sets after a canonical sort.
+"""
+from __future__ import annotations
+
+import enum
+
+import numpy as np
+import torch
+
+from .. import _lib as L
+
+
+class SFCCurveType(enum.IntEnum):
+    """dynamis_state/include/dynamis_state/partitioner.hpp:54 (bindings :96-98)."""
+
+    Morton = 0
+    Hilbert = 1
+
+
+def _check(cond: bool, msg: str) -> None:
+    if not cond:
+        raise RuntimeError(msg)
+
+
+def _shape(t: torch.Tensor) -> str:
+    return "[" + ", ".join(str(s) for s in t.shape) + "]"
+
+
+def _validate(pos, cell, pbc, radius, max_num_neighbors=None, target_indices=None):
+    """radius_graph.cpp:15-37 and :78-86 (messages kept)."""
+    _check(isinstance(pos, torch.Tensor) and pos.is_cuda, "pos must be a CUDA tensor")
+    _check(pos.dim() == 2 and pos.size(1) == 3,
+           f"pos must have shape [N, 3], got {_shape(pos)}")
+    _check(pos.dtype in (torch.float32, torch.float64),
+           f"pos must be float32 or float64, got {pos.dtype}")
+    cell = torch.as_tensor(cell)
+    _check(cell.dim() == 2 and cell.size(0) == 3 and cell.size(1) == 3,
+           f"cell must have shape [3, 3], got {_shape(cell)}")
+    pbc = torch.as_tensor(pbc)
+    _check(pbc.dim() == 1 and pbc.size(0) == 3, f"pbc must have shape [3], got {_shape(pbc)}")
+    _check(float(radius) > 0.0, f"radius must be positive, got {float(radius)}")
+    if max_num_neighbors is not None:
+        _check(int(max_num_neighbors) >= 0,
+               f"max_num_neighbors must be non-negative, got {int(max_num_neighbors)}")
+    if target_indices is not None:
+        ti = target_indices
+        _check(ti.device == pos.device, "target_indices must be on the same device as pos")
+        _check(ti.dim() == 1, f"target_indices must be 1-D, got shape {list(ti.shape)}")
+        _check(ti.dtype == torch.int64, f"target_indices must be int64, got {ti.dtype}")
+        target_indices = ti.contiguous()
+    return pos.contiguous(), cell, pbc, target_indices
+
+
+def _desc(pos, cell, pbc, radius, target_indices):
+    d = L.GraphDesc()
+    d.n_atoms = pos.size(0)
+    d.has_targets = 0 if target_indices is None else 1
+    d.n_targets = 0 if target_indices is None else target_indices.size(0)
+    d.pos_dtype = L.DG_F64 if pos.dtype == torch.float64 else L.DG_F32
+    # The reference casts the cell to float32 (radius_graph.cpp:24); with float64
+    # positions the cell is kept in float64.
+    c = cell.detach().to(device="cpu", dtype=pos.dtype).to(torch.float64).reshape(-1).tolist()
+    for k in range(9):
+        d.cell[k] = c[k]
+    pb = pbc.detach().to("cpu").to(torch.bool).tolist()
+    for k in range(3):
+        d.pbc[k] = 1 if pb[k] else 0
+    d.radius = float(radius)
+    return d
+
+
+def _empty(device, n_target):
+    return (torch.empty((2, 0), dtype=torch.long, device=device),
+            torch.empty((0, 3), dtype=torch.float32, device=device),
+            torch.zeros(1, dtype=torch.long, device=device),
+            torch.zeros(n_target, dtype=torch.int32, device=device))
+
+
+def build_graph(pos, cell, pbc, radius, target_indices=None, counts_only=False,
+                return_vectors=False, vector_dtype=None):
+    """Core build shared by every entry point (validated inputs).
+
+    Returns (edge_index [2,E] int64, cell_shifts [E,3] float32, num_neighbors_image [1]
+    int64, neighbor_counts [N_target] int32[, edge_vec [E,3], edge_dist [E]]).
+    """
+    lib = L.lib()
+    dev = pos.device
+    n = pos.size(0)
+    nt = n if target_indices is None else target_indices.size(0)
+    vdt = vector_dtype or pos.dtype
+    if n == 0 or nt == 0:
+        out = _empty(dev, nt)
+        if return_vectors:
+            out = out + (torch.empty((0, 3), dtype=vdt, device=dev), torch.empty(0, dtype=vdt, device=dev))
+        return out
+    d = _desc(pos, cell, pbc, radius, target_indices)
+    wsb = lib.dg_graph_workspace_size(d)
+    if wsb == 0:
+        raise RuntimeError(lib.dg_last_error().decode())
+    with torch.cuda.device(dev):
+        s = L.stream_of(dev)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        counts = torch.empty(nt, dtype=torch.int32, device=dev)
+        L.check(lib.dg_graph_count(d, L.ptr(pos), L.ptr(target_indices), L.ptr(ws), wsb,
+                                   L.ptr(counts), s), "radius_graph_pbc")
+        if counts_only:
+            return None, None, None, counts
+        E = L._i64(0)
+        fl = L._i64(0)
+        L.check(lib.dg_graph_read_totals(d, L.ptr(ws), E, fl, s), "radius_graph_pbc")
+        E = int(E.value)
+        edge_index = torch.empty((2, E), dtype=torch.long, device=dev)
+        shifts = torch.empty((E, 3), dtype=torch.float32, device=dev)
+        vec = dist = None
+        if return_vectors:
+            vec = torch.empty((E, 3), dtype=vdt, device=dev)
+            dist = torch.empty(E, dtype=vdt, device=dev)
+        if E > 0:
+            src_ptr = edge_index.data_ptr()
+            L.check(lib.dg_graph_write(
+                d, L.ptr(pos), L.ptr(target_indices), L.ptr(ws), wsb, E,
+                L.ctypes.c_void_p(src_ptr), L.ctypes.c_void_p(src_ptr + 8 * E), L.ptr(shifts),
+                L.ptr(vec), L.ptr(dist), L.DG_F64 if vdt == torch.float64 else L.DG_F32, s),
+                "radius_graph_pbc")
+        nn = torch.full((1,), E, dtype=torch.long, device=dev)
+        out = (edge_index, shifts, nn, counts)
+        if return_vectors:
+            out = out + (vec, dist)
+        return out
+
+
+def _r32(radius) -> float:
+    # the reference binds radius as C++ float (radius_graph.cpp:7)
+    return float(np.float32(radius))
+
+
+def radius_graph_pbc(pos, cell, pbc, radius, max_num_neighbors, enforce_max_strictly):
+    """(edge_index [2,E] int64, cell_offsets [E,3] float32, num_neighbors_image [1] int64).
+
+    radius_graph.cpp:7-49.  max_num_neighbors / enforce_max_strictly are validated and
+    ignored, exactly as the reference (radius_graph_kernels.cu:771-775).
+    """
+    pos, cell, pbc, _ = _validate(pos, cell, pbc, radius, max_num_neighbors)
+    ei, co, nn, _c = build_graph(pos, cell, pbc, _r32(radius))
+    return ei, co, nn
+
+
+def radius_graph_pbc_ex(pos, cell, pbc, radius, max_num_neighbors, enforce_max_strictly,
+                        target_indices=None):
+    """(edge_index, cell_shifts, num_neighbors_image, neighbor_counts[N_target] int32).
+
+    radius_graph.cpp:51-92: only ``target_indices`` atoms are targets; sources are all
+    atoms; ids are global; neighbor_counts is in target_indices order.
+    """
+    pos, cell, pbc, ti = _validate(pos, cell, pbc, radius, max_num_neighbors, target_indices)
+    return build_graph(pos, cell, pbc, _r32(radius), ti)
+
+
+def radius_graph_pbc_counts_ex(pos, cell, pbc, radius, target_indices=None):
+    """neighbor_counts[N_target] int32 only, no host sync (radius_graph.cpp:94-127)."""
+    pos, cell, pbc, ti = _validate(pos, cell, pbc, radius, None, target_indices)
+    return build_graph(pos, cell, pbc, _r32(radius), ti, counts_only=True)[3]
+
+
+def radius_graph_pbc_vectors(pos, cell, pbc, radius, target_indices=None, vector_dtype=None):
+    """Extension: also returns the canonical edge vectors v = pos[src] + S.cell - pos[dst]
+    and distances |v| (fp64 exact, or fp32 correctly rounded from fp64).
+
+    Returns (edge_index, cell_shifts, num_neighbors_image, neighbor_counts, edge_vec,
+    edge_dist).  radius is used as given (not rounded to fp32).
+    """
+    pos, cell, pbc, ti = _validate(pos, cell, pbc, radius, None, target_indices)
+    return build_graph(pos, cell, pbc, float(radius), ti, return_vectors=True,
+                       vector_dtype=vector_dtype)
+
+
+def filter_edges_to_radius(edges, cell_shifts, pos, cell, radius):
+    """Order-preserving filter to ``radius`` (dist_graph_ops.cpp:5-35, kernels :16-102).
+
+    Keeps edge e iff |pos[src] + cell_shifts[e] @ cell - pos[dst]|^2 <= radius^2 with the
+    canonical fp64 evaluation, so filter(build(r + skin), r) == build(r) as edge sets.
+    Returns (edges', cell_shifts'), cell_shifts' keeps its dtype.
+    """
+    _check(isinstance(edges, torch.Tensor) and edges.is_cuda, "edges must be a CUDA tensor")
+    _check(edges.dim() == 2 and edges.size(0) == 2,
+           f"edges must have shape [2, E], got {list(edges.shape)}")
+    _check(edges.dtype == torch.int64, f"edges must be int64, got {edges.dtype}")
+    E = edges.size(1)
+    _check(cell_shifts.dim() == 2 and cell_shifts.size(1) == 3,
+           f"cell_shifts must have shape [E, 3], got {list(cell_shifts.shape)}")
+    _check(cell_shifts.size(0) == E,
+           f"cell_shifts rows ({cell_shifts.size(0)}) must equal number of edges E ({E})")
+    _check(isinstance(pos, torch.Tensor) and pos.is_cuda, "pos must be a CUDA tensor")
+    _check(pos.dim() == 2 and pos.size(1) == 3, f"pos must have shape [N, 3], got {list(pos.shape)}")
+    _check(pos.dtype in (torch.float32, torch.float64),
+           f"pos must be float32 or float64, got {pos.dtype}")
+    cell = torch.as_tensor(cell)
+    _check(cell.dim() == 2 and cell.size(0) == 3 and cell.size(1) == 3,
+           f"cell must have shape [3, 3], got {list(cell.shape)}")
+    _check(float(radius) > 0.0, f"radius must be positive, got {float(radius)}")
+    if E == 0:
+        return edges, cell_shifts
+    lib = L.lib()
+    dev = pos.device
+    edges = edges.contiguous()
+    pos = pos.contiguous()
+    sh = cell_shifts.contiguous()
+    if sh.dtype == torch.float32:
+        sdt = L.DG_F32
+    elif sh.dtype == torch.float64:
+        sdt = L.DG_F64
+    else:
+        sh = sh.to(torch.int64)
+        sdt = L.DG_I64
+    c = cell.detach().to(device="cpu", dtype=pos.dtype).to(torch.float64).contiguous()
+    cbuf = (L.ctypes.c_double * 9)(*c.reshape(-1).tolist())
+    wsb = lib.dg_filter_workspace_size(E)
+    with torch.cuda.device(dev):
+        s = L.stream_of(dev)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        keep = torch.empty(E, dtype=torch.int64, device=dev)
+        nk = torch.empty(1, dtype=torch.int64, device=dev)
+        base = edges.data_ptr()
+        L.check(lib.dg_filter_edges_to_radius(
+            L.ptr(pos), L.DG_F64 if pos.dtype == torch.float64 else L.DG_F32, pos.size(0), cbuf,
+            float(radius), L.ctypes.c_void_p(base), L.ctypes.c_void_p(base + 8 * E), L.ptr(sh), sdt,
+            E, L.ptr(keep), L.ptr(nk), L.ptr(ws), wsb, s), "filter_edges_to_radius")
+        k = int(nk.item())
+        idx = keep[:k]
+        return edges.index_select(1, idx).contiguous(), cell_shifts.index_select(0, idx).contiguous()
+
+
+def sfc_keys(pos, curve_type=SFCCurveType.Morton):
+    """SFC keys of every atom, int64 [N] (sfc_kernels.cu:19-109, bounds :196-198)."""
+    _check(isinstance(pos, torch.Tensor) and pos.is_cuda, "pos must be a CUDA tensor")
+    _check(pos.dim() == 2 and pos.size(1) == 3, f"pos must have shape [N, 3], got {_shape(pos)}")
+    _check(pos.dtype == torch.float32, f"pos must be float32, got {pos.dtype}")
+    ct = int(curve_type)
+    _check(ct in (0, 1), f"curve_type must be 0 (Morton) or 1 (Hilbert), got {ct}")
+    lib = L.lib()
+    pos = pos.contiguous()
+    n = pos.size(0)
+    keys = torch.empty(n, dtype=torch.int64, device=pos.device)
+    if n == 0:
+        return keys
+    wsb = lib.dg_sfc_workspace_size(n)
+    with torch.cuda.device(pos.device):
+        ws = torch.empty(wsb, dtype=torch.uint8, device=pos.device)
+        L.check(lib.dg_sfc_keys(L.ptr(pos), n, ct, L.ptr(keys), L.ptr(ws), wsb,
+                                L.stream_of(pos.device)), "sfc_keys")
+    return keys
+
+
+def sfc_order(keys):
+    """Stable ascending permutation of int64 keys (replaces at::sort, sfc_kernels.cu:224)."""
+    _check(keys.is_cuda and keys.dtype == torch.int64 and keys.dim() == 1,
+           "keys must be a 1-D int64 CUDA tensor")
+    lib = L.lib()
+    keys = keys.contiguous()
+    n = keys.size(0)
+    perm = torch.empty(n, dtype=torch.int64, device=keys.device)
+    if n == 0:
+        return perm
+    wsb = lib.dg_sfc_workspace_size(n)
+    with torch.cuda.device(keys.device):
+        ws = torch.empty(wsb, dtype=torch.uint8, device=keys.device)
+        L.check(lib.dg_sfc_order(L.ptr(keys), n, L.ptr(perm), L.ptr(ws), wsb,
+                                 L.stream_of(keys.device)), "sfc_order")
+    return perm
+
+
+def sfc_partition_cuda(pos, weights, W, curve_type):
+    """Partition labels int64 [N] (sfc.cpp:9-32 / sfc_kernels.cu:178-251).
+
+    ``weights`` is None (unweighted) or [N] integer-valued; W >= 1; curve_type 0 / 1.
+    """
+    _check(isinstance(pos, torch.Tensor) and pos.is_cuda, "pos must be a CUDA tensor")
+    _check(pos.dim() == 2 and pos.size(1) == 3,
+           f"pos must have shape [N, 3], got [{pos.size(0)}, {pos.size(1) if pos.dim() > 1 else 0}]")
+    _check(pos.dtype == torch.float32, f"pos must be float32, got {pos.dtype}")
+    _check(int(W) >= 1, f"W must be >= 1, got {int(W)}")
+    ct = int(curve_type)
+    _check(ct in (0, 1), f"curve_type must be 0 (Morton) or 1 (Hilbert), got {ct}")
+    n = pos.size(0)
+    dev = pos.device
+    if weights is not None:
+        _check(weights.is_cuda, "weights must be a CUDA tensor")
+        _check(weights.dim() == 1 and weights.size(0) == n,
+               f"weights must have shape [N], got [{weights.size(0)}]")
+        weights = weights.to(torch.int64).contiguous()
+    if int(W) == 1:
+        return torch.zeros(n, dtype=torch.int64, device=dev)
+    keys = sfc_keys(pos, ct)
+    perm = sfc_order(keys)
+    labels = torch.empty(n, dtype=torch.int64, device=dev)
+    if n == 0:
+        return labels
+    lib = L.lib()
+    wsb = lib.dg_sfc_workspace_size(n)
+    with torch.cuda.device(dev):
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        L.check(lib.dg_sfc_labels(L.ptr(perm), n, int(W), L.ptr(weights), L.ptr(labels), L.ptr(ws),
+                                  wsb, L.stream_of(dev)), "sfc_partition_cuda")
+    return labels

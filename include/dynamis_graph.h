@@ -1,0 +1,149 @@
+/*
+ * dynamis_graph.h -- C ABI of the gfx950 (MI355X) neighbour-graph library
+ * (libdynamis_graph.so, built from dynamis_amd/csrc/).
+ *
+ * Plain pointers and sizes only.  Device pointers are HIP device addresses; every call
+ * is asynchronous on the given stream unless stated otherwise.  Calls never allocate
+ * device memory: the caller passes a workspace of dg_graph_workspace_size() bytes.
+ * Status codes are returned instead of exceptions; dg_last_error() holds the message of
+ * the last failure on the calling thread.
+ *
+ * Contract of the edge set (shared by every entry point):
+ *   (src, dst, S) is an edge iff S is integer, S_d = floor(f_dst,d) - floor(f_src,d) on
+ *   non-periodic axes, and 1e-8f < d2 <= radius^2 with the fp64 canonical
+ *       v  = (p_src - p_dst) + S . cell,   d2 = |v|^2
+ *   (fixed operation order, see dynamis_amd/csrc/dg_common.hpp).  f = p . cell^-1.
+ *   This is the set the reference's cell list enumerates
+ *   (dynamis_state/src/csrc/graph/radius_graph_kernels.cu:18-442), with the predicate
+ *   evaluated in fp64 instead of fp32.
+ *
+ * References are file:line in Dynamis-MD/Dynamis.
+ */
+#ifndef DYNAMIS_GRAPH_H
+#define DYNAMIS_GRAPH_H
+
+#include <stddef.h>
+#include <stdint.h>
+
+#include <hip/hip_runtime_api.h>
+
+#ifdef __cplusplus
+extern "C" {
+#endif
+
+typedef enum {
+    DG_OK = 0,
+    DG_ERR_INVALID = 1,   /* bad argument (shape, radius, singular cell, ...) */
+    DG_ERR_WORKSPACE = 2, /* workspace too small */
+    DG_ERR_HIP = 3,       /* HIP runtime error (launch, copy) */
+    DG_ERR_RANGE = 4,     /* data-dependent: atom > 255 cells outside the cell, NaN
+                             position or target index out of range (reported by
+                             dg_graph_read_totals) */
+    DG_ERR_CAPACITY = 5   /* edge capacity smaller than the edge count */
+} dg_status;
+
+typedef enum { DG_F32 = 0, DG_F64 = 1 } dg_dtype;
+
+/* Status flag bits of dg_graph_read_totals(). */
+#define DG_FLAG_RANGE 1
+#define DG_FLAG_NONFINITE 2
+#define DG_FLAG_CAPACITY 4
+#define DG_FLAG_TARGET 8
+
+/* Description of one radius-graph build.
+ * Mirrors the arguments of radius_graph_pbc_ex (dynamis_state/src/csrc/graph/
+ * radius_graph.cpp:51-92): pos [n_atoms,3], cell [3,3] with lattice vectors as rows,
+ * pbc [3], radius, target_indices [n_targets] (NULL -> all atoms are targets). */
+typedef struct dg_graph_desc {
+    int64_t n_atoms;
+    int64_t n_targets; /* ignored when has_targets == 0 */
+    int32_t has_targets;
+    int32_t pos_dtype; /* dg_dtype */
+    double cell[9];
+    uint8_t pbc[3];
+    uint8_t pad_[5];
+    double radius;
+} dg_graph_desc;
+
+/* Bytes of device workspace needed by dg_graph_count / dg_graph_write for this
+ * description; 0 on invalid input (see dg_last_error).  Host only. */
+size_t dg_graph_workspace_size(const dg_graph_desc* desc);
+
+/* Stage 1 of a build: SFC reorder of the atoms into the cell list (Morton tile order),
+ * per-target degree count and the edge-offset scan.
+ * Replaces radius_graph_pbc_counts_ex (radius_graph.cpp:94-127) and the count half of
+ * radius_graph_pbc_cuda_impl_ex (radius_graph_kernels.cu:480-846).
+ *   pos          device, [n_atoms,3] of pos_dtype, row-major
+ *   target_idx   device int64 [n_targets] or NULL
+ *   counts_out   device int32 [n_targets] (caller order) or NULL
+ * The total edge count and status flags stay in the workspace; read them with
+ * dg_graph_read_totals (one device->host copy and stream sync). */
+dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                         void* workspace, size_t workspace_bytes, int32_t* counts_out,
+                         hipStream_t stream);
+
+/* Synchronous: copies {total_edges, flags} out of the workspace (waits for the stream).
+ * Returns DG_ERR_RANGE if a data-dependent error flag is set. */
+dg_status dg_graph_read_totals(const dg_graph_desc* desc, const void* workspace,
+                               int64_t* total_edges, int64_t* flags, hipStream_t stream);
+
+/* Stage 2 of a build (after dg_graph_count on the same workspace, inputs unchanged):
+ * writes every edge.  Replaces the B4 write of radius_graph_kernels.cu:848-933.
+ *   edge_src, edge_dst   device int64 [capacity]  (edge_index[0], edge_index[1])
+ *   cell_shift           device float32 [capacity,3]  (integer-valued; "cell_offsets")
+ *   edge_vec             device [capacity,3] of vec_dtype or NULL (canonical v)
+ *   edge_dist            device [capacity] of vec_dtype or NULL (sqrt(d2))
+ * Edges are grouped by target in the SFC processing order; within a target the order
+ * is fixed (deterministic) but unspecified.  Tiles that would overrun `capacity` are
+ * skipped and DG_FLAG_CAPACITY is raised. */
+dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                         void* workspace, size_t workspace_bytes, int64_t capacity,
+                         int64_t* edge_src, int64_t* edge_dst, float* cell_shift, void* edge_vec,
+                         void* edge_dist, int32_t vec_dtype, hipStream_t stream);
+
+/* Order-preserving filter of an edge list to radius (keep iff d2 <= radius^2, canonical
+ * fp64 d2).  Replaces filter_edges_to_radius (dist_graph_ops.cpp:5-35,
+ * dist_graph_ops_kernels.cu:16-43,62-102).
+ *   edge_src/edge_dst int64 [n_edges], cell_shift [n_edges,3] of shift_dtype
+ *   keep_idx out int64 [n_edges]: indices of kept edges, ascending
+ *   n_kept   out int64 (device, one value)
+ *   workspace of dg_filter_workspace_size(n_edges) bytes */
+size_t dg_filter_workspace_size(int64_t n_edges);
+dg_status dg_filter_edges_to_radius(const void* pos, int32_t pos_dtype, int64_t n_atoms,
+                                    const double* cell, double radius, const int64_t* edge_src,
+                                    const int64_t* edge_dst, const void* cell_shift,
+                                    int32_t shift_dtype, int64_t n_edges, int64_t* keep_idx,
+                                    int64_t* n_kept, void* workspace, size_t workspace_bytes,
+                                    hipStream_t stream);
+
+/* SFC keys exactly as partition/sfc_kernels.cu:19-109 (curve 0 = Morton 21-bit,
+ * 1 = "Hilbert" order 7), normalised by the global min / range of pos
+ * (sfc_kernels.cu:196-198, range 0 -> 1).  pos fp32 [n,3]; keys int64 [n];
+ * workspace of dg_sfc_workspace_size(n) bytes.  Replaces the key stage of
+ * sfc_partition_cuda_impl (sfc_kernels.cu:178-213). */
+size_t dg_sfc_workspace_size(int64_t n);
+dg_status dg_sfc_keys(const float* pos, int64_t n, int32_t curve, int64_t* keys, void* workspace,
+                      size_t workspace_bytes, hipStream_t stream);
+
+/* Stable ascending sort permutation of int64 keys (ties keep index order).
+ * Replaces at::sort(sfc_keys) in sfc_kernels.cu:224.  perm int64 [n]. */
+dg_status dg_sfc_order(const int64_t* keys, int64_t n, int64_t* perm, void* workspace,
+                       size_t workspace_bytes, hipStream_t stream);
+
+/* Partition labels from a permutation: unweighted closed form (sfc_kernels.cu:114-136)
+ * or exact int64 weighted cut (sfc_kernels.cu:153-173, weights int64 [n] or NULL).
+ * labels int64 [n]. */
+dg_status dg_sfc_labels(const int64_t* perm, int64_t n, int64_t n_parts, const int64_t* weights,
+                        int64_t* labels, void* workspace, size_t workspace_bytes,
+                        hipStream_t stream);
+
+/* Message of the last failure on this thread ("" if none). */
+const char* dg_last_error(void);
+
+/* Library version string. */
+const char* dg_version(void);
+
+#ifdef __cplusplus
+}
+#endif
+#endif /* DYNAMIS_GRAPH_H */

@@ -1,0 +1,512 @@
+/*
+ * graph_oracle.c -- CPU restatement of Dynamis's PBC radius-graph build and SFC keys.
+ *
+ * TEST INFRASTRUCTURE ONLY.  Nothing in the product (dynamis_amd/) links, loads or
+ * calls this file.  Only tests/, __graft_entry__.smoke() and bench.py's cpu_baseline
+ * leg use it, and only as the checker / the reported CPU baseline.
+ *
+ * It follows the reference algorithm stage by stage (paths relative to the reference
+ * repository root, dynamis_state/src/csrc/...):
+ *   geometry          graph/radius_graph_kernels.cu:515-594  (d_face, rep, cutoff_frac, cell^-1)
+ *   wrap              graph/radius_graph_kernels.cu:596-605  (frac = pos.cell^-1, floor, wrap)
+ *   selective images  graph/radius_graph_kernels.cu:18-141   (count/write PBC images)
+ *   grid              graph/radius_graph_kernels.cu:662-714  (bbox +-0.01, cell = r/1.99, sort)
+ *   count / write     graph/radius_graph_kernels.cu:197-258, 282-303, 320-442
+ *   outputs           graph/radius_graph_kernels.cu:925-933
+ *   filter            graph/dist_graph_ops_kernels.cu:16-43, 62-102
+ *   SFC keys          partition/sfc_kernels.cu:19-109, 196-198 (fp32 arithmetic kept)
+ *
+ * with one deliberate change that defines the build's contract: the cutoff predicate
+ * is evaluated in fp64 on the ORIGINAL positions and the integer output shift S,
+ *     v  = (p_src - p_tgt) + S.C,    d2 = |v|^2,    edge iff 1e-8f < d2 <= r^2,
+ * with the fixed operation order of dg_canon_d2() below (explicit fma, no contraction;
+ * build with -ffp-contract=off).  The reference evaluates the same predicate in fp32
+ * on wrapped coordinates (radius_graph_kernels.cu:247-250, 399-400).
+ *
+ * The wrap (floor of the fractional coordinate) is evaluated in fp64 by the same fixed
+ * formula (dg_canon_frac) so that non-periodic axes -- which the reference wraps too,
+ * radius_graph_kernels.cu:603-605 -- get the same integer shift everywhere.
+ */
+#include <math.h>
+#include <stdint.h>
+#include <stdlib.h>
+#include <string.h>
+#ifdef _OPENMP
+#include <omp.h>
+#endif
+
+#define ORC_SELF_THR ((double)1e-8f) /* radius_graph_kernels.cu:250 literal 1e-8f */
+
+typedef struct {
+    double C[9];    /* rows = lattice vectors */
+    double Cinv[9]; /* frac_j = sum_i p_i * Cinv[i*3+j] */
+    double d_face[3];
+    double cf[3];
+    int rep[3];
+    int pbc[3];
+    double vol;
+} orc_geom;
+
+/* radius_graph_kernels.cu:515-594, in fp64. */
+static int orc_geometry(const double* cell, const uint8_t* pbc, double r, orc_geom* g)
+{
+    const double *a0 = cell, *a1 = cell + 3, *a2 = cell + 6;
+    double c12[3] = {a1[1] * a2[2] - a1[2] * a2[1], a1[2] * a2[0] - a1[0] * a2[2],
+                     a1[0] * a2[1] - a1[1] * a2[0]};
+    double c20[3] = {a2[1] * a0[2] - a2[2] * a0[1], a2[2] * a0[0] - a2[0] * a0[2],
+                     a2[0] * a0[1] - a2[1] * a0[0]};
+    double c01[3] = {a0[1] * a1[2] - a0[2] * a1[1], a0[2] * a1[0] - a0[0] * a1[2],
+                     a0[0] * a1[1] - a0[1] * a1[0]};
+    double vol = a0[0] * c12[0] + a0[1] * c12[1] + a0[2] * c12[2];
+    if (!(fabs(vol) > 0.0) || !isfinite(vol)) return -1;
+    memcpy(g->C, cell, 9 * sizeof(double));
+    g->vol = vol;
+    double av = fabs(vol);
+    const double* cs[3] = {c12, c20, c01};
+    for (int d = 0; d < 3; d++) {
+        double n = sqrt(cs[d][0] * cs[d][0] + cs[d][1] * cs[d][1] + cs[d][2] * cs[d][2]);
+        g->d_face[d] = av / n;
+        g->cf[d] = r / g->d_face[d];
+        g->pbc[d] = pbc[d] ? 1 : 0;
+        g->rep[d] = pbc[d] ? (int)ceil(g->cf[d]) : 0;
+    }
+    for (int i = 0; i < 3; i++)
+        for (int j = 0; j < 3; j++) g->Cinv[i * 3 + j] = cs[j][i] / vol;
+    return 0;
+}
+
+/* Canonical fractional coordinate (fixed fp64 order). */
+static inline double dg_canon_frac(const double p[3], const double* Cinv, int j)
+{
+    return fma(p[2], Cinv[6 + j], fma(p[1], Cinv[3 + j], p[0] * Cinv[j]));
+}
+
+/* Canonical edge vector and squared distance (fixed fp64 order). */
+static inline double dg_canon_d2(const double ps[3], const double pt[3], const int S[3],
+                                 const double* C, double v[3])
+{
+    for (int a = 0; a < 3; a++) {
+        double sc = fma((double)S[2], C[6 + a], fma((double)S[1], C[3 + a], (double)S[0] * C[a]));
+        v[a] = (ps[a] - pt[a]) + sc;
+    }
+    return fma(v[2], v[2], fma(v[1], v[1], v[0] * v[0]));
+}
+
+static inline void load_pos(const void* pos, int f64, int64_t i, double p[3])
+{
+    if (f64) {
+        const double* q = (const double*)pos + 3 * i;
+        p[0] = q[0]; p[1] = q[1]; p[2] = q[2];
+    } else {
+        const float* q = (const float*)pos + 3 * i;
+        p[0] = q[0]; p[1] = q[1]; p[2] = q[2];
+    }
+}
+
+typedef struct {
+    int64_t n, nt;          /* atoms, targets */
+    orc_geom g;
+    double r, r2;
+    int f64;
+    const void* pos;
+    const int64_t* tgt;     /* NULL = all atoms */
+    int* flr;               /* [n*3] floor(frac) */
+    double* pw;             /* [n*3] wrapped positions (fp64) */
+    /* images, sorted by grid cell */
+    int64_t m;
+    int64_t* img_orig;      /* [m] */
+    int* img_shift;         /* [m*3] */
+    double* img_pos;        /* [m*3] */
+    int gn[3];
+    double gmin[3], res;
+    int* cstart;            /* [ncell+1] */
+    int64_t* tord;          /* target processing order: list of target slots (cell-sorted) */
+    int* tcell;             /* [nt*3] target cell coords (per slot) */
+} orc_ctx;
+
+typedef struct { int64_t key; int64_t idx; } kv;
+static int kv_cmp(const void* a, const void* b)
+{
+    const kv* x = (const kv*)a; const kv* y = (const kv*)b;
+    if (x->key != y->key) return x->key < y->key ? -1 : 1;
+    return x->idx < y->idx ? -1 : (x->idx > y->idx);
+}
+
+static void ctx_free(orc_ctx* c)
+{
+    free(c->flr); free(c->pw); free(c->img_orig); free(c->img_shift); free(c->img_pos);
+    free(c->cstart); free(c->tord); free(c->tcell);
+}
+
+static int ctx_build(orc_ctx* c, const void* pos, int f64, int64_t n, const double* cell,
+                     const uint8_t* pbc, double radius, const int64_t* tgt, int64_t nt)
+{
+    memset(c, 0, sizeof(*c));
+    c->n = n; c->nt = tgt ? nt : n; c->f64 = f64; c->pos = pos; c->tgt = tgt;
+    c->r = radius; c->r2 = radius * radius;
+    if (orc_geometry(cell, pbc, radius, &c->g)) return -1;
+    const orc_geom* g = &c->g;
+    c->flr = (int*)malloc(sizeof(int) * 3 * (n ? n : 1));
+    c->pw = (double*)malloc(sizeof(double) * 3 * (n ? n : 1));
+    /* wrap: radius_graph_kernels.cu:596-605 (all axes, periodic or not) */
+    for (int64_t i = 0; i < n; i++) {
+        double p[3]; load_pos(pos, f64, i, p);
+        int f[3];
+        for (int j = 0; j < 3; j++) f[j] = (int)floor(dg_canon_frac(p, g->Cinv, j));
+        for (int a = 0; a < 3; a++) {
+            double sh = fma((double)f[2], g->C[6 + a], fma((double)f[1], g->C[3 + a], (double)f[0] * g->C[a]));
+            c->pw[3 * i + a] = p[a] - sh;
+        }
+        memcpy(c->flr + 3 * i, f, sizeof f);
+    }
+    /* selective images: radius_graph_kernels.cu:18-141.  The face tests use the fp64
+     * wrapped fraction with a 1e-9 safety margin (a superset of needed images; the exact
+     * predicate below decides membership). */
+    int64_t* cnt = (int64_t*)calloc(n + 1, sizeof(int64_t));
+    const double eps = 1e-9;
+    for (int pass = 0; pass < 2; pass++) {
+        int64_t m = 0;
+        for (int64_t i = 0; i < n; i++) {
+            double p[3]; load_pos(pos, f64, i, p);
+            double s[3];
+            for (int j = 0; j < 3; j++) {
+                double fr = dg_canon_frac(p, g->Cinv, j);
+                s[j] = fr - floor(fr);
+            }
+            for (int dx = -g->rep[0]; dx <= g->rep[0]; dx++)
+                for (int dy = -g->rep[1]; dy <= g->rep[1]; dy++)
+                    for (int dz = -g->rep[2]; dz <= g->rep[2]; dz++) {
+                        int dd[3] = {dx, dy, dz}, ok = 1;
+                        for (int d = 0; d < 3 && ok; d++) {
+                            if (!g->pbc[d] && dd[d] != 0) ok = 0;
+                            else if (dd[d] > 0 && !(s[d] < g->cf[d] + eps)) ok = 0;
+                            else if (dd[d] < 0 && !(s[d] > 1.0 - g->cf[d] - eps)) ok = 0;
+                        }
+                        if (!ok) continue;
+                        if (pass == 1) {
+                            c->img_orig[m] = i;
+                            memcpy(c->img_shift + 3 * m, dd, sizeof dd);
+                            for (int a = 0; a < 3; a++)
+                                c->img_pos[3 * m + a] = c->pw[3 * i + a] + dx * g->C[a] + dy * g->C[3 + a] + dz * g->C[6 + a];
+                        }
+                        m++;
+                    }
+        }
+        if (pass == 0) {
+            c->m = m;
+            c->img_orig = (int64_t*)malloc(sizeof(int64_t) * (m ? m : 1));
+            c->img_shift = (int*)malloc(sizeof(int) * 3 * (m ? m : 1));
+            c->img_pos = (double*)malloc(sizeof(double) * 3 * (m ? m : 1));
+        }
+    }
+    free(cnt);
+    /* grid: radius_graph_kernels.cu:662-692 (bbox of images U targets, +-0.01, r/1.99) */
+    double lo[3] = {INFINITY, INFINITY, INFINITY}, hi[3] = {-INFINITY, -INFINITY, -INFINITY};
+    for (int64_t k = 0; k < c->m; k++)
+        for (int a = 0; a < 3; a++) {
+            double v = c->img_pos[3 * k + a];
+            if (v < lo[a]) lo[a] = v;
+            if (v > hi[a]) hi[a] = v;
+        }
+    for (int64_t i = 0; i < n; i++)
+        for (int a = 0; a < 3; a++) {
+            double v = c->pw[3 * i + a];
+            if (v < lo[a]) lo[a] = v;
+            if (v > hi[a]) hi[a] = v;
+        }
+    c->res = radius / 1.99;
+    for (int a = 0; a < 3; a++) {
+        lo[a] -= 0.01; hi[a] += 0.01;
+        c->gmin[a] = lo[a];
+        int v = (int)ceil((hi[a] - lo[a]) / c->res);
+        c->gn[a] = v < 1 ? 1 : v;
+    }
+    int64_t ncell = (int64_t)c->gn[0] * c->gn[1] * c->gn[2];
+    /* assign + stable sort of images by linear cell id: radius_graph_kernels.cu:146-171, 707-714 */
+    kv* keys = (kv*)malloc(sizeof(kv) * (c->m ? c->m : 1));
+    for (int64_t k = 0; k < c->m; k++) {
+        int cc[3];
+        for (int a = 0; a < 3; a++) {
+            int v = (int)floor((c->img_pos[3 * k + a] - c->gmin[a]) / c->res);
+            cc[a] = v < 0 ? 0 : (v >= c->gn[a] ? c->gn[a] - 1 : v);
+        }
+        keys[k].key = cc[0] + (int64_t)cc[1] * c->gn[0] + (int64_t)cc[2] * c->gn[0] * c->gn[1];
+        keys[k].idx = k;
+    }
+    qsort(keys, c->m, sizeof(kv), kv_cmp);
+    int64_t* o2 = (int64_t*)malloc(sizeof(int64_t) * (c->m ? c->m : 1));
+    int* s2 = (int*)malloc(sizeof(int) * 3 * (c->m ? c->m : 1));
+    double* p2 = (double*)malloc(sizeof(double) * 3 * (c->m ? c->m : 1));
+    c->cstart = (int*)calloc(ncell + 1, sizeof(int));
+    for (int64_t k = 0; k < c->m; k++) {
+        int64_t src = keys[k].idx;
+        o2[k] = c->img_orig[src];
+        memcpy(s2 + 3 * k, c->img_shift + 3 * src, 3 * sizeof(int));
+        memcpy(p2 + 3 * k, c->img_pos + 3 * src, 3 * sizeof(double));
+        c->cstart[keys[k].key + 1]++;
+    }
+    for (int64_t q = 0; q < ncell; q++) c->cstart[q + 1] += c->cstart[q];
+    free(c->img_orig); free(c->img_shift); free(c->img_pos);
+    c->img_orig = o2; c->img_shift = s2; c->img_pos = p2;
+    /* targets: cell coords + stable sort by cell id (radius_graph_kernels.cu:731-769) */
+    kv* tk = (kv*)malloc(sizeof(kv) * (c->nt ? c->nt : 1));
+    c->tcell = (int*)malloc(sizeof(int) * 3 * (c->nt ? c->nt : 1));
+    for (int64_t t = 0; t < c->nt; t++) {
+        int64_t a = tgt ? tgt[t] : t;
+        int cc[3];
+        for (int d = 0; d < 3; d++) {
+            int v = (int)floor((c->pw[3 * a + d] - c->gmin[d]) / c->res);
+            cc[d] = v < 0 ? 0 : (v >= c->gn[d] ? c->gn[d] - 1 : v);
+        }
+        memcpy(c->tcell + 3 * t, cc, sizeof cc);
+        tk[t].key = cc[0] + (int64_t)cc[1] * c->gn[0] + (int64_t)cc[2] * c->gn[0] * c->gn[1];
+        tk[t].idx = t;
+    }
+    qsort(tk, c->nt, sizeof(kv), kv_cmp);
+    c->tord = (int64_t*)malloc(sizeof(int64_t) * (c->nt ? c->nt : 1));
+    for (int64_t t = 0; t < c->nt; t++) c->tord[t] = tk[t].idx;
+    free(tk); free(keys);
+    return 0;
+}
+
+/* Scan one target (slot t): count neighbours, or write them if out != NULL.
+ * radius_graph_kernels.cu:197-258 (count) and 320-442 + 282-303 (write/emit). */
+static int64_t scan_target(const orc_ctx* c, int64_t t, int64_t base, int64_t* src, int64_t* dst,
+                           int32_t* shift, double* vec, double* d2out)
+{
+    const int pad = (int)floor(c->r / c->res) + 1; /* = 2 */
+    int64_t a = c->tgt ? c->tgt[t] : t;
+    double pt[3]; load_pos(c->pos, c->f64, a, pt);
+    const int* ft = c->flr + 3 * a;
+    const int* tc = c->tcell + 3 * t;
+    int64_t k = 0;
+    for (int dz = -pad; dz <= pad; dz++) {
+        int nz = tc[2] + dz;
+        if (nz < 0 || nz >= c->gn[2]) continue;
+        for (int dy = -pad; dy <= pad; dy++) {
+            int ny = tc[1] + dy;
+            if (ny < 0 || ny >= c->gn[1]) continue;
+            for (int dx = -pad; dx <= pad; dx++) {
+                int nx = tc[0] + dx;
+                if (nx < 0 || nx >= c->gn[0]) continue;
+                int64_t cid = nx + (int64_t)ny * c->gn[0] + (int64_t)nz * c->gn[0] * c->gn[1];
+                for (int s = c->cstart[cid]; s < c->cstart[cid + 1]; s++) {
+                    int64_t so = c->img_orig[s];
+                    const int* fs = c->flr + 3 * so;
+                    int S[3];
+                    for (int d = 0; d < 3; d++) S[d] = c->img_shift[3 * s + d] + ft[d] - fs[d];
+                    double ps[3], v[3];
+                    load_pos(c->pos, c->f64, so, ps);
+                    double d2 = dg_canon_d2(ps, pt, S, c->g.C, v);
+                    if (d2 <= c->r2 && d2 > ORC_SELF_THR) {
+                        if (src) {
+                            int64_t o = base + k;
+                            src[o] = so; dst[o] = a;
+                            shift[3 * o] = S[0]; shift[3 * o + 1] = S[1]; shift[3 * o + 2] = S[2];
+                            if (vec) { vec[3 * o] = v[0]; vec[3 * o + 1] = v[1]; vec[3 * o + 2] = v[2]; }
+                            if (d2out) d2out[o] = d2;
+                        }
+                        k++;
+                    }
+                }
+            }
+        }
+    }
+    return k;
+}
+
+/* ---------------------------------------------------------------------------------- */
+/* Exported API (ctypes).                                                              */
+
+typedef struct orc_graph {
+    orc_ctx c;
+    int64_t* cnt_slot; /* per processing slot */
+    int64_t* off;      /* exclusive offsets per processing slot, [nt+1] */
+} orc_graph;
+
+/* Build the graph structure and count; returns handle (NULL on error).
+ * counts_user[t] = degree of target t in caller order (radius_graph_kernels.cu:925-931). */
+void* orc_graph_count(const void* pos, int f64, int64_t n, const double* cell, const uint8_t* pbc,
+                      double radius, const int64_t* tgt, int64_t nt, int32_t* counts_user,
+                      int64_t* total, int threads)
+{
+#ifdef _OPENMP
+    if (threads > 0) omp_set_num_threads(threads);
+#else
+    (void)threads;
+#endif
+    orc_graph* h = (orc_graph*)calloc(1, sizeof(orc_graph));
+    if (ctx_build(&h->c, pos, f64, n, cell, pbc, radius, tgt, nt)) { free(h); return NULL; }
+    int64_t T = h->c.nt;
+    h->cnt_slot = (int64_t*)malloc(sizeof(int64_t) * (T ? T : 1));
+    h->off = (int64_t*)malloc(sizeof(int64_t) * (T + 1));
+#pragma omp parallel for schedule(dynamic, 256)
+    for (int64_t q = 0; q < T; q++) h->cnt_slot[q] = scan_target(&h->c, h->c.tord[q], 0, 0, 0, 0, 0, 0);
+    h->off[0] = 0;
+    for (int64_t q = 0; q < T; q++) h->off[q + 1] = h->off[q] + h->cnt_slot[q];
+    if (counts_user)
+        for (int64_t q = 0; q < T; q++) counts_user[h->c.tord[q]] = (int32_t)h->cnt_slot[q];
+    *total = h->off[T];
+    return h;
+}
+
+/* Write edges (reference order: targets in cell-sorted order, then stencil order). */
+void orc_graph_write(void* hv, int64_t* src, int64_t* dst, int32_t* shift, double* vec, double* d2)
+{
+    orc_graph* h = (orc_graph*)hv;
+    int64_t T = h->c.nt;
+#pragma omp parallel for schedule(dynamic, 256)
+    for (int64_t q = 0; q < T; q++) scan_target(&h->c, h->c.tord[q], h->off[q], src, dst, shift, vec, d2);
+}
+
+void orc_graph_free(void* hv)
+{
+    orc_graph* h = (orc_graph*)hv;
+    if (!h) return;
+    ctx_free(&h->c);
+    free(h->cnt_slot); free(h->off); free(h);
+}
+
+int64_t orc_graph_num_images(void* hv) { return ((orc_graph*)hv)->c.m; }
+
+/* Canonical geometry exposed for tests: Cinv[9], d_face[3], rep[3]. */
+int orc_geometry_export(const double* cell, const uint8_t* pbc, double r, double* Cinv,
+                        double* d_face, int32_t* rep)
+{
+    orc_geom g;
+    if (orc_geometry(cell, pbc, r, &g)) return -1;
+    memcpy(Cinv, g.Cinv, sizeof g.Cinv);
+    memcpy(d_face, g.d_face, sizeof g.d_face);
+    for (int d = 0; d < 3; d++) rep[d] = g.rep[d];
+    return 0;
+}
+
+/* Canonical edge vectors / squared distances for a given edge list (int shifts). */
+void orc_edge_vectors(const void* pos, int f64, const double* cell, int64_t E, const int64_t* src,
+                      const int64_t* dst, const int32_t* shift, double* vec, double* d2)
+{
+#pragma omp parallel for schedule(static)
+    for (int64_t e = 0; e < E; e++) {
+        double ps[3], pt[3], v[3];
+        load_pos(pos, f64, src[e], ps);
+        load_pos(pos, f64, dst[e], pt);
+        double q = dg_canon_d2(ps, pt, shift + 3 * e, cell, v);
+        if (vec) { vec[3 * e] = v[0]; vec[3 * e + 1] = v[1]; vec[3 * e + 2] = v[2]; }
+        if (d2) d2[e] = q;
+    }
+}
+
+/* filter_edges_to_radius (dist_graph_ops_kernels.cu:16-43, 62-102): keep iff d2 <= r^2,
+ * order preserving.  Writes keep[E] (0/1); returns number kept. */
+int64_t orc_filter_edges(const void* pos, int f64, const double* cell, double radius, int64_t E,
+                         const int64_t* src, const int64_t* dst, const int32_t* shift, uint8_t* keep)
+{
+    double r2 = radius * radius;
+    int64_t kept = 0;
+#pragma omp parallel for schedule(static) reduction(+ : kept)
+    for (int64_t e = 0; e < E; e++) {
+        double ps[3], pt[3], v[3];
+        load_pos(pos, f64, src[e], ps);
+        load_pos(pos, f64, dst[e], pt);
+        keep[e] = dg_canon_d2(ps, pt, shift + 3 * e, cell, v) <= r2;
+        kept += keep[e];
+    }
+    return kept;
+}
+
+/* ---------------------------------------------------------------------------------- */
+/* SFC keys: partition/sfc_kernels.cu:19-109 and bounds :196-198, fp32 arithmetic.      */
+
+static uint64_t spread_bits_21(uint32_t v)
+{
+    /* bit i of v -> bit 3i of the result, written as a plain loop */
+    uint64_t r = 0;
+    for (int i = 0; i < 21; i++) r |= (uint64_t)((v >> i) & 1u) << (3 * i);
+    return r;
+}
+
+/* pos fp32 [n,3]; pos_min / pos_range as the reference computes them (fp32 min, max-min,
+ * range==0 -> 1). */
+void orc_sfc_bounds(const float* pos, int64_t n, float* mn, float* range)
+{
+    for (int a = 0; a < 3; a++) {
+        float lo = INFINITY, hi = -INFINITY;
+        for (int64_t i = 0; i < n; i++) {
+            float v = pos[3 * i + a];
+            if (v < lo) lo = v;
+            if (v > hi) hi = v;
+        }
+        mn[a] = lo;
+        float rg = hi - lo;
+        range[a] = rg > 0.0f ? rg : 1.0f;
+    }
+}
+
+void orc_morton_keys(const float* pos, int64_t n, const float* mn, const float* range, int64_t* keys)
+{
+    const uint32_t gmax = (1u << 21) - 1;
+    for (int64_t i = 0; i < n; i++) {
+        uint32_t q[3];
+        for (int a = 0; a < 3; a++) {
+            float x = (pos[3 * i + a] - mn[a]) / range[a];
+            float y = x * (float)gmax;
+            uint32_t u = (uint32_t)y;
+            q[a] = u < gmax ? u : gmax;
+        }
+        uint64_t k = spread_bits_21(q[0]) | (spread_bits_21(q[1]) << 1) | (spread_bits_21(q[2]) << 2);
+        keys[i] = (int64_t)k;
+    }
+}
+
+void orc_hilbert_keys(const float* pos, int64_t n, const float* mn, const float* range, int64_t* keys)
+{
+    const int order = 7, gmax = (1 << order) - 1;
+    for (int64_t i = 0; i < n; i++) {
+        int c[3];
+        for (int a = 0; a < 3; a++) {
+            float x = (pos[3 * i + a] - mn[a]) / range[a];
+            int v = (int)(x * (float)gmax);
+            c[a] = v < 0 ? 0 : (v > gmax ? gmax : v);
+        }
+        int64_t res = 0;
+        for (int b = 0; b < order; b++) {
+            int xb = (c[0] >> b) & 1, yb = (c[1] >> b) & 1, zb = (c[2] >> b) & 1;
+            int nx = xb, ny = yb, nz = zb;
+            if (b > 0) {
+                /* sfc_kernels.cu:94-101 */
+                nx = xb ? zb : xb;
+                ny = xb ? yb : (yb ? zb : yb);
+                nz = xb ? yb : (yb ? xb : (zb ? yb : zb));
+            }
+            res |= ((int64_t)nx << (3 * b)) | ((int64_t)ny << (3 * b + 1)) | ((int64_t)nz << (3 * b + 2));
+        }
+        keys[i] = res;
+    }
+}
+
+/* Partition labels from a permutation: sfc_kernels.cu:114-136 (unweighted) and
+ * :153-173 (weighted, exact int64 prefix sum of the sorted integer weights). */
+void orc_sfc_labels(const int64_t* perm, int64_t n, int64_t W, const int64_t* weights, int64_t* labels)
+{
+    if (W == 1) { for (int64_t i = 0; i < n; i++) labels[i] = 0; return; }
+    if (!weights) {
+        int64_t base = n / W, rem = n % W, thr = rem * (base + 1);
+        for (int64_t i = 0; i < n; i++) {
+            int64_t p = i < thr ? i / (base + 1) : rem + (i - thr) / base;
+            if (p > W - 1) p = W - 1;
+            labels[perm[i]] = p;
+        }
+        return;
+    }
+    int64_t* cs = (int64_t*)malloc(sizeof(int64_t) * (n ? n : 1));
+    int64_t acc = 0;
+    for (int64_t i = 0; i < n; i++) { acc += weights[perm[i]]; cs[i] = acc; }
+    int64_t total = n ? cs[n - 1] : 0;
+    for (int64_t i = 0; i < n; i++) {
+        int64_t p = total > 0 ? (cs[i] * W) / total : 0;
+        if (p < 0) p = 0;
+        if (p > W - 1) p = W - 1;
+        labels[perm[i]] = p;
+    }
+    free(cs);
+}

@@ -1,0 +1,59 @@
+"""GPU parity of the SFC keys, the stable order and the partition labels vs the oracle
+(sfc_kernels.cu:19-173 restated in oracle/graph_oracle.c)."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dynamis_amd.dynamis_state import dynamis_state_impl as impl
+
+pytestmark = pytest.mark.gpu
+
+
+def _pos(n, seed, lo=-40.0, hi=60.0):
+    return np.random.default_rng(seed).uniform(lo, hi, (n, 3)).astype(np.float32)
+
+
+@pytest.mark.parametrize("curve", [0, 1])
+@pytest.mark.parametrize("n", [1, 17, 100_000])
+def test_keys_bit_exact(cuda, curve, n):
+    print(f"\n[case] sfc keys curve={curve} n={n}", flush=True)
+    p = _pos(n, n + curve)
+    k = impl.sfc_keys(torch.from_numpy(p).to(cuda), curve).cpu().numpy()
+    want = oracle.morton_keys(p) if curve == 0 else oracle.hilbert_keys(p)
+    assert np.array_equal(k, want)
+
+
+def test_keys_degenerate_axis(cuda):
+    p = _pos(1000, 5)
+    p[:, 1] = 3.25  # zero range -> 1
+    for curve in (0, 1):
+        k = impl.sfc_keys(torch.from_numpy(p).to(cuda), curve).cpu().numpy()
+        want = oracle.morton_keys(p) if curve == 0 else oracle.hilbert_keys(p)
+        assert np.array_equal(k, want)
+
+
+@pytest.mark.parametrize("n", [1, 1000, 300_001])
+def test_order_is_stable_argsort(cuda, n):
+    print(f"\n[case] sfc order n={n}", flush=True)
+    rng = np.random.default_rng(n)
+    keys = rng.integers(-2 ** 40, 2 ** 40, n) // 1000  # plenty of ties
+    keys[: n // 3] = rng.integers(0, 5, n // 3)
+    perm = impl.sfc_order(torch.from_numpy(keys).to(cuda)).cpu().numpy()
+    assert np.array_equal(perm, np.argsort(keys, kind="stable"))
+    same = np.full(n, 7, np.int64)
+    assert np.array_equal(impl.sfc_order(torch.from_numpy(same).to(cuda)).cpu().numpy(), np.arange(n))
+
+
+@pytest.mark.parametrize("curve", [0, 1])
+@pytest.mark.parametrize("W", [1, 3, 8])
+def test_partition_labels(cuda, curve, W):
+    p = _pos(50_000, 9)
+    pt = torch.from_numpy(p).to(cuda)
+    lab = impl.sfc_partition_cuda(pt, None, W, curve).cpu().numpy()
+    keys = oracle.morton_keys(p) if curve == 0 else oracle.hilbert_keys(p)
+    perm = np.argsort(keys, kind="stable")
+    assert np.array_equal(lab, oracle.sfc_labels(perm, W))
+    w = np.random.default_rng(1).integers(0, 200, 50_000)
+    labw = impl.sfc_partition_cuda(pt, torch.from_numpy(w).to(cuda), W, curve).cpu().numpy()
+    assert np.array_equal(labw, oracle.sfc_labels(perm, W, w))
