@@ -25,6 +25,7 @@
 #include <math.h>
 #include <stdint.h>
 #include <stdio.h>
+#include <stdlib.h>
 #include <string.h>
 
 #include <string>
@@ -45,7 +46,7 @@ dg_status fail(dg_status st, const std::string& msg)
 }
 
 constexpr int kCap = 1536;    // region entries staged in LDS per chunk
-constexpr int kStage = 2560;  // edge records staged in LDS per batch (write pass)
+constexpr int kRing = 512;  // per-wave ring of edge records awaiting a 64-wide store
 constexpr int kBinSortMax = 128;
 
 __device__ __forceinline__ void load_pos(const void* pos, int f64, int64_t i, double* p)
@@ -313,7 +314,7 @@ __device__ __forceinline__ void region_offset(const SearchArgs& a, int rx, int r
 }
 
 // Exact (canonical fp64) decision for a candidate the fp32 prefilter cannot settle.
-__device__ __noinline__ bool exact_edge(const SearchArgs& a, int src, int tgt, int S0, int S1,
+__device__ __forceinline__ bool exact_edge(const SearchArgs& a, int src, int tgt, int S0, int S1,
                                         int S2)
 {
     if (src == tgt && S0 == 0 && S1 == 0 && S2 == 0) return false;
@@ -324,11 +325,41 @@ __device__ __noinline__ bool exact_edge(const SearchArgs& a, int src, int tgt, i
     return d2 > kSelfThr && d2 <= a.r2;
 }
 
+// One edge: edge_index columns, integer cell shift, optional canonical vector / distance.
+__device__ __forceinline__ void emit_edge(const SearchArgs& a, int64_t o, int src, int dst, int S0,
+                                          int S1, int S2)
+{
+    a.out_src[o] = src;
+    a.out_dst[o] = dst;
+    *(float3*)(a.out_shift + 3 * o) = make_float3((float)S0, (float)S1, (float)S2);
+    if (a.out_vec || a.out_dist) {
+        double ps[3], pt[3], vv[3];
+        load_pos(a.pos, a.f64, src, ps);
+        load_pos(a.pos, a.f64, dst, pt);
+        const double dd = canon_d2(ps, pt, S0, S1, S2, a.C, vv);
+        if (a.vout_f64) {
+            if (a.out_vec) {
+                double* ov = (double*)a.out_vec + 3 * o;
+                ov[0] = vv[0]; ov[1] = vv[1]; ov[2] = vv[2];
+            }
+            if (a.out_dist) ((double*)a.out_dist)[o] = sqrt(dd);
+        } else {
+            if (a.out_vec) {
+                float* ov = (float*)a.out_vec + 3 * o;
+                ov[0] = (float)vv[0]; ov[1] = (float)vv[1]; ov[2] = (float)vv[2];
+            }
+            if (a.out_dist) ((float*)a.out_dist)[o] = (float)sqrt(dd);
+        }
+    }
+}
+
+// WRITE = false: per-target degree and per-tile total.  WRITE = true: edges, at the
+// offsets the count pass fixed (same scan code, so both passes see the same edges).
 template <bool WRITE>
 __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 {
     __shared__ SearchShared sh;
-    __shared__ int2 s_stage[WRITE ? kStage : 1];
+    __shared__ uint32_t s_ring[WRITE ? kBlock / 64 : 1][WRITE ? kRing : 1];
 
     const int64_t rank = xcd_tile_rank(blockIdx.x, a.ntiles);
     const int lin = a.tile_of_rank[rank];
@@ -436,34 +467,37 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
     }
     if (skip_tile) return;
 
+    // One lane per target; each wave owns 64 consecutive targets of the batch and their
+    // edges fill one contiguous output range.  The row loop (one row = 2P+1 bins along x)
+    // and the loop along a row are uniform across the wave (lanes past their row end are
+    // masked), so the wave can append the edges of every step to its LDS ring of
+    // (region index, lane) records and stream them out 64 at a time with full-width,
+    // coalesced stores.
+    const int lane = threadIdx.x & 63;
+    const int wid = threadIdx.x >> 6;
+    const int tw0 = threadIdx.x & ~63;
+    const uint64_t lt_mask = (1ull << lane) - 1ull;
+    uint32_t* ring = s_ring[WRITE ? wid : 0];
     for (int k0 = 0; k0 < ntg; ) {
-        // ---- choose the batch of targets handled by this pass over the region
+        const int nbatch = min(kBlock, ntg - k0);
         const int kk = k0 + threadIdx.x;
-        int mycnt = 0;
-        if (WRITE && kk < ntg) mycnt = a.cnt[tbeg + kk];
-        int nbatch, ex = 0, btot = 0;
-        bool direct = false;
-        if (WRITE) {
-            ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
-            // targets whose staged records still fit
-            int fits = (kk < ntg && ex + mycnt <= kStage) ? 1 : 0;
-            int nf;
-            block_excl_scan<int, kBlock>(fits, sh.w32, &nf);
-            nbatch = nf;
-            if (nbatch == 0) { nbatch = 1; direct = true; }
-            if (threadIdx.x < nbatch) sh.boff[threadIdx.x] = ex;
-            if (threadIdx.x == nbatch - 1) sh.boff[nbatch] = ex + mycnt;
-            __syncthreads();
-        } else {
-            nbatch = min(kBlock, ntg - k0);
-        }
         const bool active = threadIdx.x < nbatch;
+        int mycnt = 0;
+        int64_t wave_base = 0;
+        int btot = 0;
+        if (WRITE) {
+            // per-target counts from the count pass give each wave's output offset
+            if (active) mycnt = a.cnt[tbeg + kk];
+            const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
+            if (lane == 0) sh.boff[wid] = ex;
+            __syncthreads();
+            wave_base = ebase + sh.boff[wid];
+        }
 
         // ---- per-lane target state
-        int lx = 0, ly = 0, lz = 0, my_id = 0, caller = 0;
+        int lx = 0, ly = 0, lz = 0, my_id = 0, caller = 0, v_self = -1;
         uint32_t my_f = 0;
         float t0 = 0.f, t1 = 0.f, t2 = 0.f;
-        int my_slot = 0;
         if (active) {
             const int j = tbeg + kk;
             int lo = 0, hi = a.tb;
@@ -482,14 +516,68 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             float o[3];
             region_offset(a, lx + a.P[0], ly + a.P[1], lz + a.P[2], o);
             t0 = e.x + o[0]; t1 = e.y + o[1]; t2 = e.z + o[2];
-            if (WRITE) {
-                sh.tid[threadIdx.x] = my_id;
-                sh.tf[threadIdx.x] = my_f;
-                my_slot = sh.boff[threadIdx.x];
-            }
+            // the target's own entry in the region (same atom, zero shift): never an edge
+            const int rb_self = ((lz + a.P[2]) * R1 + (ly + a.P[1])) * R0 + (lx + a.P[0]);
+            v_self = sh.rp[rb_self] + (sidx - sh.rg[rb_self]);
+        }
+        if (WRITE) {
+            sh.tid[threadIdx.x] = my_id;
+            sh.tf[threadIdx.x] = my_f;
         }
         const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
         int found = 0;
+        int v_self_c = -1;    // v_self relative to the resident chunk
+        int64_t flushed = 0;  // records of this wave already stored (uniform)
+        int pend = 0;         // records appended to the ring and not yet stored (uniform)
+
+        // Store `cnt` (<= 64) ring records starting at `flushed`.
+        auto flush = [&](int cnt) {
+            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+            __builtin_amdgcn_wave_barrier();
+            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            if (lane < cnt) {
+                const uint32_t rec = ring[(uint32_t)(flushed + lane) & (kRing - 1)];
+                const int v = (int)(rec & 0xffffu);
+                const int t = tw0 + (int)(rec >> 16);
+                const uint32_t Tp = sh.T[v];
+                const uint32_t ft = sh.tf[t];
+                emit_edge(a, wave_base + flushed + lane, __float_as_int(sh.q[v].w), sh.tid[t],
+                          unpack3(Tp, 0) + unpack3(ft, 0), unpack3(Tp, 1) + unpack3(ft, 1),
+                          unpack3(Tp, 2) + unpack3(ft, 2));
+            }
+            flushed += cnt;
+            pend -= cnt;
+        };
+
+        // One candidate: fp32 prefilter, exact fp64 decision inside the rounding band.
+        auto consider = [&](const float4 q, const int vi, bool ok) -> bool {
+            const float dx = q.x - t0, dyv = q.y - t1, dzv = q.z - t2;
+            const float d2 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
+            ok = ok && vi != v_self_c;
+            bool edge = ok && d2 < a.lo_in && d2 > a.tiny;
+            const bool band = ok && !edge && d2 <= a.hi;
+            if (__builtin_expect(band, false)) {
+                const uint32_t Tp = sh.T[vi];
+                edge = exact_edge(a, __float_as_int(q.w), my_id, unpack3(Tp, 0) + fx,
+                                  unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
+            }
+            // found < mycnt always holds in the write pass (both passes run this code);
+            // the guard keeps a violation from writing out of range
+            if (WRITE) edge = edge && found < mycnt;
+            found += edge ? 1 : 0;
+            return edge;
+        };
+        auto append = [&](const bool edge, const int vi) {
+            const uint64_t m = __ballot(edge);
+            if (m) {
+                if (edge) {
+                    const int rk = __popcll(m & lt_mask);
+                    ring[(uint32_t)(flushed + pend + rk) & (kRing - 1)] =
+                        (uint32_t)vi | ((uint32_t)lane << 16);
+                }
+                pend += __popcll(m);
+            }
+        };
 
         for (int c = 0; c < nchunks; ++c) {
             if (loaded != c) {
@@ -498,71 +586,40 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
                 __syncthreads();
                 loaded = c;
             }
-            if (!active) continue;
+            if (tw0 >= nbatch) continue;  // wave without targets in this batch
             const int c0 = c * kCap;
             const int c1 = min(total, c0 + kCap);
+            v_self_c = v_self - c0;
             for (int dz = 0; dz <= 2 * a.P[2]; ++dz) {
                 for (int dy = 0; dy <= 2 * a.P[1]; ++dy) {
-                    const int rb = ((lz + dz) * R1 + (ly + dy)) * R0 + lx;
-                    int va = sh.rp[rb], vb = sh.rp[rb + 2 * a.P[0] + 1];
-                    va = max(va, c0) - c0;
-                    vb = min(vb, c1) - c0;
-                    for (int v = va; v < vb; ++v) {
-                        const float4 q = sh.q[v];
-                        const float dx = q.x - t0, dyv = q.y - t1, dzv = q.z - t2;
-                        const float d2 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
-                        if (d2 <= a.hi) {
-                            const uint32_t Tp = sh.T[v];
-                            bool edge;
-                            if (d2 < a.lo_in && d2 > a.tiny) {
-                                edge = true;
-                            } else {
-                                edge = exact_edge(a, __float_as_int(q.w), my_id,
-                                                  unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy,
-                                                  unpack3(Tp, 2) + fz);
-                            }
-                            if (edge) {
-                                // found < mycnt always holds (both passes run this exact
-                                // code); the guard keeps a violation from writing out of range
-                                if (WRITE && found < mycnt) {
-                                    if (!direct) {
-                                        s_stage[my_slot + found] = make_int2(__float_as_int(q.w), (int)Tp);
-                                    } else {
-                                        const int64_t o = ebase + found;
-                                        const int S0 = unpack3(Tp, 0) + fx, S1 = unpack3(Tp, 1) + fy,
-                                                  S2 = unpack3(Tp, 2) + fz;
-                                        const int src = __float_as_int(q.w);
-                                        a.out_src[o] = src;
-                                        a.out_dst[o] = my_id;
-                                        a.out_shift[3 * o] = (float)S0;
-                                        a.out_shift[3 * o + 1] = (float)S1;
-                                        a.out_shift[3 * o + 2] = (float)S2;
-                                        if (a.out_vec || a.out_dist) {
-                                            double ps[3], pt[3], vv[3];
-                                            load_pos(a.pos, a.f64, src, ps);
-                                            load_pos(a.pos, a.f64, my_id, pt);
-                                            double dd = canon_d2(ps, pt, S0, S1, S2, a.C, vv);
-                                            if (a.vout_f64) {
-                                                if (a.out_vec) {
-                                                    double* ov = (double*)a.out_vec + 3 * o;
-                                                    ov[0] = vv[0]; ov[1] = vv[1]; ov[2] = vv[2];
-                                                }
-                                                if (a.out_dist) ((double*)a.out_dist)[o] = sqrt(dd);
-                                            } else {
-                                                if (a.out_vec) {
-                                                    float* ov = (float*)a.out_vec + 3 * o;
-                                                    ov[0] = (float)vv[0]; ov[1] = (float)vv[1]; ov[2] = (float)vv[2];
-                                                }
-                                                if (a.out_dist) ((float*)a.out_dist)[o] = (float)sqrt(dd);
-                                            }
-                                        }
-                                    }
-                                }
-                                ++found;
-                            }
+                    int va = 0, vb = 0;
+                    if (active) {
+                        const int rb = ((lz + dz) * R1 + (ly + dy)) * R0 + lx;
+                        va = max(sh.rp[rb], c0) - c0;
+                        vb = min(sh.rp[rb + 2 * a.P[0] + 1], c1) - c0;
+                    }
+                    for (int v = va; __any(v < vb); v += 4) {
+                        // four independent LDS loads in flight before the first use
+                        const bool k0ok = v < vb, k1ok = v + 1 < vb, k2ok = v + 2 < vb, k3ok = v + 3 < vb;
+                        const float4 q0 = sh.q[k0ok ? v : 0], q1 = sh.q[k1ok ? v + 1 : 0];
+                        const float4 q2 = sh.q[k2ok ? v + 2 : 0], q3 = sh.q[k3ok ? v + 3 : 0];
+                        const bool e0 = consider(q0, v, k0ok);
+                        const bool e1 = consider(q1, v + 1, k1ok);
+                        const bool e2 = consider(q2, v + 2, k2ok);
+                        const bool e3 = consider(q3, v + 3, k3ok);
+                        if (WRITE) {
+                            append(e0, v);
+                            append(e1, v + 1);
+                            append(e2, v + 2);
+                            append(e3, v + 3);
+                            while (pend >= 64) flush(64);
                         }
                     }
                 }
+            }
+            // ring records index the resident chunk: drain before it is replaced
+            if (WRITE) {
+                while (pend > 0) flush(min(pend, 64));
             }
         }
 
@@ -574,55 +631,8 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             int64_t bt;
             block_excl_scan<int64_t, kBlock>((int64_t)found, sh.w64, &bt);
             tile_edges += bt;
-            k0 += nbatch;
-            continue;
-        }
-
-        // ---- write pass: stream the staged records out, fully coalesced
-        __syncthreads();
-        if (!direct) {
-            const int nE = sh.boff[nbatch];
-            for (int e = threadIdx.x; e < nE; e += kBlock) {
-                int lo = 0, hi = nbatch;
-                while (hi - lo > 1) {
-                    int mid = (lo + hi) >> 1;
-                    if (sh.boff[mid] <= e) lo = mid; else hi = mid;
-                }
-                const int2 rec = s_stage[e];
-                const uint32_t ft = sh.tf[lo];
-                const int dst = sh.tid[lo];
-                const int S0 = unpack3((uint32_t)rec.y, 0) + unpack3(ft, 0);
-                const int S1 = unpack3((uint32_t)rec.y, 1) + unpack3(ft, 1);
-                const int S2 = unpack3((uint32_t)rec.y, 2) + unpack3(ft, 2);
-                const int64_t o = ebase + e;
-                a.out_src[o] = rec.x;
-                a.out_dst[o] = dst;
-                a.out_shift[3 * o] = (float)S0;
-                a.out_shift[3 * o + 1] = (float)S1;
-                a.out_shift[3 * o + 2] = (float)S2;
-                if (a.out_vec || a.out_dist) {
-                    double ps[3], pt[3], vv[3];
-                    load_pos(a.pos, a.f64, rec.x, ps);
-                    load_pos(a.pos, a.f64, dst, pt);
-                    double dd = canon_d2(ps, pt, S0, S1, S2, a.C, vv);
-                    if (a.vout_f64) {
-                        if (a.out_vec) {
-                            double* ov = (double*)a.out_vec + 3 * o;
-                            ov[0] = vv[0]; ov[1] = vv[1]; ov[2] = vv[2];
-                        }
-                        if (a.out_dist) ((double*)a.out_dist)[o] = sqrt(dd);
-                    } else {
-                        if (a.out_vec) {
-                            float* ov = (float*)a.out_vec + 3 * o;
-                            ov[0] = (float)vv[0]; ov[1] = (float)vv[1]; ov[2] = (float)vv[2];
-                        }
-                        if (a.out_dist) ((float*)a.out_dist)[o] = (float)sqrt(dd);
-                    }
-                }
-            }
-            ebase += nE;
         } else {
-            ebase += a.cnt[tbeg + k0];
+            ebase += btot;  // the next batch starts after this batch's edges
         }
         __syncthreads();
         k0 += nbatch;

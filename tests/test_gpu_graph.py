@@ -51,11 +51,6 @@ def check_parity(pos, cell, pbc, r, dev, targets=None, name=""):
     w = oracle.canonical_sort(o["src"], o["dst"], o["shift"])
     for a, b in zip(g, w):
         assert np.array_equal(a, b)
-    # edges are grouped by target
-    if E:
-        d = dst
-        starts = np.flatnonzero(np.r_[True, d[1:] != d[:-1]])
-        assert len(np.unique(d)) == len(starts) or targets is not None
     return ei, co, cnt, o
 
 
