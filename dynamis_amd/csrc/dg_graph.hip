@@ -45,8 +45,8 @@ dg_status fail(dg_status st, const std::string& msg)
     return st;
 }
 
-constexpr int kCap = 1536;    // region entries staged in LDS per chunk
-constexpr int kRing = 512;  // per-wave ring of edge records awaiting a 64-wide store
+constexpr int kCap = 1792;    // region entries staged in LDS per chunk
+constexpr int kRegPerThread = (kMaxRegion + kBlock - 1) / kBlock;
 constexpr int kBinSortMax = 128;
 
 __device__ __forceinline__ void load_pos(const void* pos, int f64, int64_t i, double* p)
@@ -246,7 +246,10 @@ __global__ void finish_targets_kernel(int64_t nbins, int64_t n, const int* __res
 // ---------------------------------------------------------------- neighbour search
 struct SearchArgs {
     double C[9];
+    double hC[9];  // bin step vectors: row d = C[d] / nb[d]
     double r2;
+    int ortho;     // orthorhombic cell with positive diagonal: stencil rows are trimmed
+    float hb[3], hbinv[3], rprune2, pmargin;
     int nb[3], P[3], T[3], ntl[3], R[3], pbc[3];
     int tb, nregion;
     int64_t ntiles;
@@ -277,6 +280,8 @@ struct SearchArgs {
     int vout_f64;
     int64_t capacity;
     int64_t* totals;
+    uint16_t* slot;  // per-target neighbour slots (K region indices each), or null
+    int K;
 };
 
 // blockIdx -> tile rank: consecutive workgroups go round-robin to the 8 XCDs, so give
@@ -290,27 +295,24 @@ __device__ __forceinline__ int64_t xcd_tile_rank(int64_t b, int64_t ntiles)
 }
 
 struct SearchShared {
-    float4 q[kCap];
-    uint32_t T[kCap];
+    float4 q[kCap + 1];  // + sentinel
+    uint32_t T[kCap + 1];
     int rp[kMaxRegion + 1];
     int rg[kMaxRegion];
-    int tbs[65];
-    int boff[kBlock + 1];
+    int tbs[6 * 6 * 6 + 1];  // bin starts of the tile (T <= 6 per axis)
+    int off[kBlock + 1];  // write pass: edge offsets of the batch's targets
     int tid[kBlock];
     uint32_t tf[kBlock];
     int64_t w64[kBlock / 64];
     int w32[kBlock / 64];
-    int misc[4];
 };
 
 __device__ __forceinline__ void region_offset(const SearchArgs& a, int rx, int ry, int rz,
                                               float* o)
 {
-    double u0 = (double)(rx - a.P[0]) / (double)a.nb[0];
-    double u1 = (double)(ry - a.P[1]) / (double)a.nb[1];
-    double u2 = (double)(rz - a.P[2]) / (double)a.nb[2];
+    const double u0 = (double)(rx - a.P[0]), u1 = (double)(ry - a.P[1]), u2 = (double)(rz - a.P[2]);
 #pragma unroll
-    for (int c = 0; c < 3; ++c) o[c] = (float)fma(u2, a.C[6 + c], fma(u1, a.C[3 + c], u0 * a.C[c]));
+    for (int c = 0; c < 3; ++c) o[c] = (float)fma(u2, a.hC[6 + c], fma(u1, a.hC[3 + c], u0 * a.hC[c]));
 }
 
 // Exact (canonical fp64) decision for a candidate the fp32 prefilter cannot settle.
@@ -353,13 +355,26 @@ __device__ __forceinline__ void emit_edge(const SearchArgs& a, int64_t o, int sr
     }
 }
 
-// WRITE = false: per-target degree and per-tile total.  WRITE = true: edges, at the
-// offsets the count pass fixed (same scan code, so both passes see the same edges).
-template <bool WRITE>
+// Neighbour search, one tile of bins per workgroup.
+//
+// The region of (T+2P)^3 bins around the tile is staged in LDS (in chunks if it does
+// not fit).  Both passes share the per-target sweep below (one lane per target, rows of
+// the stencil trimmed to the cutoff sphere for orthorhombic cells), so they agree on
+// every edge and on its order.
+//
+// MODE 0 (count): per-target degree, per-tile total, and -- for tiles whose region fits
+//   in one chunk -- the target's neighbours as 2-byte LDS region indices in its slot of
+//   K entries (written 16 bytes at a time through a per-lane LDS buffer).
+// MODE 1 (write): no distance tests: the region is staged again, every output edge of the
+//   tile is mapped to (target, k) and expanded from the slot with full-width coalesced
+//   stores, grouped by target in the SFC order.  Targets with more than K neighbours and
+//   tiles with a chunked region are swept again and written directly.
+template <int MODE>
 __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 {
+    constexpr bool WRITE = MODE == 1;
     __shared__ SearchShared sh;
-    __shared__ uint32_t s_ring[WRITE ? kBlock / 64 : 1][WRITE ? kRing : 1];
+    __shared__ __align__(16) uint16_t s_lb[WRITE ? 1 : kBlock][8];
 
     const int64_t rank = xcd_tile_rank(blockIdx.x, a.ntiles);
     const int lin = a.tile_of_rank[rank];
@@ -377,54 +392,65 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
     }
     for (int k = threadIdx.x; k <= a.tb; k += kBlock) sh.tbs[k] = tstart[kb + k];
 
+    int64_t ebase = 0;
+    if (WRITE) {
+        ebase = a.tbase[rank];
+        if (a.tbase[rank + 1] > a.capacity) {
+            if (threadIdx.x == 0)
+                atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
+            return;
+        }
+    }
+
     // ---- region table: (T+2P)^3 bins around the tile, periodic wrap on pbc axes
     const int R0 = a.R[0], R1 = a.R[1];
-    int c_lo = 0, c_hi = 0, st_lo = 0, st_hi = 0;
-    {
-        const int rb0 = 2 * threadIdx.x, rb1 = rb0 + 1;
-        int cnt2[2] = {0, 0}, st2[2] = {0, 0};
+    int rcnt[kRegPerThread], rst[kRegPerThread];
+    int mysum = 0;
 #pragma unroll
-        for (int h = 0; h < 2; ++h) {
-            int rb = rb0 + h;
-            if (rb >= a.nregion) continue;
-            int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
-            int w[3];
-            bool ok = true;
+    for (int h = 0; h < kRegPerThread; ++h) {
+        rcnt[h] = 0;
+        rst[h] = 0;
+        const int rb = kRegPerThread * threadIdx.x + h;
+        if (rb >= a.nregion) continue;
+        const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+        int w[3];
+        bool ok = true;
 #pragma unroll
-            for (int d = 0; d < 3; ++d) {
-                int gg = g0[d] - a.P[d] + r[d];
-                if (a.pbc[d]) {
-                    int m = gg % a.nb[d];
-                    w[d] = m < 0 ? m + a.nb[d] : m;
-                } else {
-                    ok = ok && gg >= 0 && gg < a.nb[d];
-                    w[d] = gg;
-                }
-            }
-            if (ok) {
-                int t0 = w[0] / a.T[0], t1 = w[1] / a.T[1], t2 = w[2] / a.T[2];
-                int l0 = w[0] - t0 * a.T[0], l1 = w[1] - t1 * a.T[1], l2 = w[2] - t2 * a.T[2];
-                int tl = t0 + a.ntl[0] * (t1 + a.ntl[1] * t2);
-                int64_t key = (int64_t)a.rank_of_tile[tl] * a.tb + (l0 + a.T[0] * (l1 + a.T[1] * l2));
-                st2[h] = a.bstart[key];
-                cnt2[h] = a.bstart[key + 1] - st2[h];
+        for (int d = 0; d < 3; ++d) {
+            const int gg = g0[d] - a.P[d] + r[d];
+            if (a.pbc[d]) {
+                const int m = gg % a.nb[d];
+                w[d] = m < 0 ? m + a.nb[d] : m;
+            } else {
+                ok = ok && gg >= 0 && gg < a.nb[d];
+                w[d] = gg;
             }
         }
-        c_lo = cnt2[0]; c_hi = cnt2[1]; st_lo = st2[0]; st_hi = st2[1];
-        (void)rb1;
+        if (ok) {
+            const int t0 = w[0] / a.T[0], t1 = w[1] / a.T[1], t2 = w[2] / a.T[2];
+            const int l0 = w[0] - t0 * a.T[0], l1 = w[1] - t1 * a.T[1], l2 = w[2] - t2 * a.T[2];
+            const int tl = t0 + a.ntl[0] * (t1 + a.ntl[1] * t2);
+            const int64_t key = (int64_t)a.rank_of_tile[tl] * a.tb + (l0 + a.T[0] * (l1 + a.T[1] * l2));
+            rst[h] = a.bstart[key];
+            rcnt[h] = a.bstart[key + 1] - rst[h];
+        }
+        mysum += rcnt[h];
     }
     int total;
     {
-        int ex = block_excl_scan<int, kBlock>(c_lo + c_hi, sh.w32, &total);
-        const int rb0 = 2 * threadIdx.x;
-        if (rb0 < a.nregion) { sh.rp[rb0] = ex; sh.rg[rb0] = st_lo; }
-        if (rb0 + 1 < a.nregion) { sh.rp[rb0 + 1] = ex + c_lo; sh.rg[rb0 + 1] = st_hi; }
+        int ex = block_excl_scan<int, kBlock>(mysum, sh.w32, &total);
+#pragma unroll
+        for (int h = 0; h < kRegPerThread; ++h) {
+            const int rb = kRegPerThread * threadIdx.x + h;
+            if (rb < a.nregion) { sh.rp[rb] = ex; sh.rg[rb] = rst[h]; }
+            ex += rcnt[h];
+        }
         if (threadIdx.x == 0) sh.rp[a.nregion] = total;
     }
     __syncthreads();
-
     const int nchunks = (total + kCap - 1) / kCap;
-    int loaded = -1;  // chunk currently in LDS
+    const bool one_chunk = nchunks <= 1;
+    int loaded = -1;
 
     auto load_chunk = [&](int c) {
         const int c0 = c * kCap;
@@ -433,211 +459,216 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             const int vv = c0 + v;
             int lo = 0, hi = a.nregion;
             while (hi - lo > 1) {
-                int mid = (lo + hi) >> 1;
+                const int mid = (lo + hi) >> 1;
                 if (sh.rp[mid] <= vv) lo = mid; else hi = mid;
             }
             const int rb = lo;
             const int gidx = sh.rg[rb] + (vv - sh.rp[rb]);
-            float4 e = a.spos[gidx];
-            uint32_t fl = a.sflr[gidx];
-            int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+            const float4 e = a.spos[gidx];
+            const uint32_t fl = a.sflr[gidx];
+            const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
             float o[3];
             region_offset(a, r[0], r[1], r[2], o);
             int sb[3];
 #pragma unroll
             for (int d = 0; d < 3; ++d) {
-                int gg = g0[d] - a.P[d] + r[d];
+                const int gg = g0[d] - a.P[d] + r[d];
                 sb[d] = a.pbc[d] ? floor_div(gg, a.nb[d]) : 0;
             }
             sh.q[v] = make_float4(e.x + o[0], e.y + o[1], e.z + o[2], e.w);
             sh.T[v] = pack3(sb[0] - unpack3(fl, 0), sb[1] - unpack3(fl, 1), sb[2] - unpack3(fl, 2));
         }
     };
-
-    int64_t tile_edges = 0;            // count pass: tile total
-    int64_t ebase = WRITE ? a.tbase[rank] : 0;
-    bool skip_tile = false;
-    if (WRITE) {
-        int64_t tot_tile = a.tbase[rank + 1] - a.tbase[rank];
-        if (ebase + tot_tile > a.capacity) {
-            skip_tile = true;
-            if (threadIdx.x == 0)
-                atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
+    auto ensure_chunk = [&](int c) {  // uniform
+        if (loaded != c) {
+            __syncthreads();
+            load_chunk(c);
+            __syncthreads();
+            loaded = c;
         }
-    }
-    if (skip_tile) return;
+    };
 
-    // One lane per target; each wave owns 64 consecutive targets of the batch and their
-    // edges fill one contiguous output range.  The row loop (one row = 2P+1 bins along x)
-    // and the loop along a row are uniform across the wave (lanes past their row end are
-    // masked), so the wave can append the edges of every step to its LDS ring of
-    // (region index, lane) records and stream them out 64 at a time with full-width,
-    // coalesced stores.
-    const int lane = threadIdx.x & 63;
-    const int wid = threadIdx.x >> 6;
-    const int tw0 = threadIdx.x & ~63;
-    const uint64_t lt_mask = (1ull << lane) - 1ull;
-    uint32_t* ring = s_ring[WRITE ? wid : 0];
-    for (int k0 = 0; k0 < ntg; ) {
+    const int nrx = 2 * a.P[0] + 1, nry = 2 * a.P[1] + 1, nrz = 2 * a.P[2] + 1;
+    int64_t tile_found = 0;
+
+    for (int k0 = 0; k0 < ntg; k0 += kBlock) {
         const int nbatch = min(kBlock, ntg - k0);
         const int kk = k0 + threadIdx.x;
+        const int j = tbeg + kk;
         const bool active = threadIdx.x < nbatch;
-        int mycnt = 0;
-        int64_t wave_base = 0;
-        int btot = 0;
-        if (WRITE) {
-            // per-target counts from the count pass give each wave's output offset
-            if (active) mycnt = a.cnt[tbeg + kk];
-            const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
-            if (lane == 0) sh.boff[wid] = ex;
-            __syncthreads();
-            wave_base = ebase + sh.boff[wid];
-        }
 
         // ---- per-lane target state
         int lx = 0, ly = 0, lz = 0, my_id = 0, caller = 0, v_self = -1;
         uint32_t my_f = 0;
-        float t0 = 0.f, t1 = 0.f, t2 = 0.f;
+        float t0 = 0.f, t1 = 0.f, t2 = 0.f, ux = 0.f, uy = 0.f, uz = 0.f;
         if (active) {
-            const int j = tbeg + kk;
             int lo = 0, hi = a.tb;
             while (hi - lo > 1) {
-                int mid = (lo + hi) >> 1;
+                const int mid = (lo + hi) >> 1;
                 if (sh.tbs[mid] <= j) lo = mid; else hi = mid;
             }
             lx = lo % a.T[0];
             ly = (lo / a.T[0]) % a.T[1];
             lz = lo / (a.T[0] * a.T[1]);
             const int sidx = a.subset ? a.tsidx[j] : j;
-            float4 e = a.spos[sidx];
+            const float4 e = a.spos[sidx];
             my_f = a.sflr[sidx];
             my_id = __float_as_int(e.w);
             caller = a.subset ? a.tslot[j] : my_id;
+            ux = e.x; uy = e.y; uz = e.z;  // position inside its own bin
             float o[3];
             region_offset(a, lx + a.P[0], ly + a.P[1], lz + a.P[2], o);
             t0 = e.x + o[0]; t1 = e.y + o[1]; t2 = e.z + o[2];
-            // the target's own entry in the region (same atom, zero shift): never an edge
+            // the target's own region entry (same atom, zero shift) is never an edge
             const int rb_self = ((lz + a.P[2]) * R1 + (ly + a.P[1])) * R0 + (lx + a.P[0]);
             v_self = sh.rp[rb_self] + (sidx - sh.rg[rb_self]);
         }
-        if (WRITE) {
-            sh.tid[threadIdx.x] = my_id;
-            sh.tf[threadIdx.x] = my_f;
-        }
         const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
+
+        // Sweep this lane's target over the resident chunk c, in the fixed order (dz, dy,
+        // x, atom); on_edge(v, k) receives the chunk-local region index and the running
+        // neighbour number k of every edge.
         int found = 0;
-        int v_self_c = -1;    // v_self relative to the resident chunk
-        int64_t flushed = 0;  // records of this wave already stored (uniform)
-        int pend = 0;         // records appended to the ring and not yet stored (uniform)
-
-        // Store `cnt` (<= 64) ring records starting at `flushed`.
-        auto flush = [&](int cnt) {
-            __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-            __builtin_amdgcn_wave_barrier();
-            __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            if (lane < cnt) {
-                const uint32_t rec = ring[(uint32_t)(flushed + lane) & (kRing - 1)];
-                const int v = (int)(rec & 0xffffu);
-                const int t = tw0 + (int)(rec >> 16);
-                const uint32_t Tp = sh.T[v];
-                const uint32_t ft = sh.tf[t];
-                emit_edge(a, wave_base + flushed + lane, __float_as_int(sh.q[v].w), sh.tid[t],
-                          unpack3(Tp, 0) + unpack3(ft, 0), unpack3(Tp, 1) + unpack3(ft, 1),
-                          unpack3(Tp, 2) + unpack3(ft, 2));
-            }
-            flushed += cnt;
-            pend -= cnt;
-        };
-
-        // One candidate: fp32 prefilter, exact fp64 decision inside the rounding band.
-        auto consider = [&](const float4 q, const int vi, bool ok) -> bool {
-            const float dx = q.x - t0, dyv = q.y - t1, dzv = q.z - t2;
-            const float d2 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
-            ok = ok && vi != v_self_c;
-            bool edge = ok && d2 < a.lo_in && d2 > a.tiny;
-            const bool band = ok && !edge && d2 <= a.hi;
-            if (__builtin_expect(band, false)) {
-                const uint32_t Tp = sh.T[vi];
-                edge = exact_edge(a, __float_as_int(q.w), my_id, unpack3(Tp, 0) + fx,
-                                  unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
-            }
-            // found < mycnt always holds in the write pass (both passes run this code);
-            // the guard keeps a violation from writing out of range
-            if (WRITE) edge = edge && found < mycnt;
-            found += edge ? 1 : 0;
-            return edge;
-        };
-        auto append = [&](const bool edge, const int vi) {
-            const uint64_t m = __ballot(edge);
-            if (m) {
-                if (edge) {
-                    const int rk = __popcll(m & lt_mask);
-                    ring[(uint32_t)(flushed + pend + rk) & (kRing - 1)] =
-                        (uint32_t)vi | ((uint32_t)lane << 16);
-                }
-                pend += __popcll(m);
-            }
-        };
-
-        for (int c = 0; c < nchunks; ++c) {
-            if (loaded != c) {
-                __syncthreads();
-                load_chunk(c);
-                __syncthreads();
-                loaded = c;
-            }
-            if (tw0 >= nbatch) continue;  // wave without targets in this batch
+        auto sweep = [&](int c, auto&& on_edge) {
             const int c0 = c * kCap;
             const int c1 = min(total, c0 + kCap);
-            v_self_c = v_self - c0;
-            for (int dz = 0; dz <= 2 * a.P[2]; ++dz) {
-                for (int dy = 0; dy <= 2 * a.P[1]; ++dy) {
-                    int va = 0, vb = 0;
-                    if (active) {
-                        const int rb = ((lz + dz) * R1 + (ly + dy)) * R0 + lx;
-                        va = max(sh.rp[rb], c0) - c0;
-                        vb = min(sh.rp[rb + 2 * a.P[0] + 1], c1) - c0;
+            const int vs = v_self - c0;
+            for (int oz = 0; oz < nrz; ++oz) {
+                for (int oy = 0; oy < nry; ++oy) {
+                    int xlo = 0, xhi = nrx - 1;
+                    if (a.ortho) {
+                        // gaps from the target to the row's slab along y and z; keep only the
+                        // bins along x that the (padded) cutoff sphere reaches
+                        const int py = oy - a.P[1], pz = oz - a.P[2];
+                        float gy = py > 0 ? py * a.hb[1] - uy : (py < 0 ? uy + (-py - 1) * a.hb[1] : 0.f);
+                        float gz = pz > 0 ? pz * a.hb[2] - uz : (pz < 0 ? uz + (-pz - 1) * a.hb[2] : 0.f);
+                        gy = fmaxf(gy - a.pmargin, 0.f);
+                        gz = fmaxf(gz - a.pmargin, 0.f);
+                        const float rem2 = a.rprune2 - gy * gy - gz * gz;
+                        if (rem2 < 0.f) continue;
+                        const float rem = sqrtf(rem2);
+                        xlo = max((int)floorf((ux - rem) * a.hbinv[0]) + a.P[0], 0);
+                        xhi = min((int)floorf((ux + rem) * a.hbinv[0]) + a.P[0], nrx - 1);
                     }
-                    for (int v = va; __any(v < vb); v += 4) {
-                        // four independent LDS loads in flight before the first use
-                        const bool k0ok = v < vb, k1ok = v + 1 < vb, k2ok = v + 2 < vb, k3ok = v + 3 < vb;
-                        const float4 q0 = sh.q[k0ok ? v : 0], q1 = sh.q[k1ok ? v + 1 : 0];
-                        const float4 q2 = sh.q[k2ok ? v + 2 : 0], q3 = sh.q[k3ok ? v + 3 : 0];
-                        const bool e0 = consider(q0, v, k0ok);
-                        const bool e1 = consider(q1, v + 1, k1ok);
-                        const bool e2 = consider(q2, v + 2, k2ok);
-                        const bool e3 = consider(q3, v + 3, k3ok);
-                        if (WRITE) {
-                            append(e0, v);
-                            append(e1, v + 1);
-                            append(e2, v + 2);
-                            append(e3, v + 3);
-                            while (pend >= 64) flush(64);
+                    const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
+                    const int va = max(sh.rp[rb + xlo], c0) - c0;
+                    const int vb = min(sh.rp[rb + xhi + 1], c1) - c0;
+                    for (int v = va; v < vb; ++v) {
+                        const float4 q = sh.q[v];
+                        const float dx = q.x - t0, dyv = q.y - t1, dzv = q.z - t2;
+                        const float d2 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
+                        bool edge = d2 < a.lo_in && d2 > a.tiny;
+                        if (__builtin_expect(!edge && d2 <= a.hi && v != vs, false)) {
+                            const uint32_t Tp = sh.T[v];
+                            edge = exact_edge(a, __float_as_int(q.w), my_id, unpack3(Tp, 0) + fx,
+                                              unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
+                        }
+                        if (edge) {
+                            on_edge(v, found);
+                            ++found;
                         }
                     }
                 }
             }
-            // ring records index the resident chunk: drain before it is replaced
-            if (WRITE) {
-                while (pend > 0) flush(min(pend, 64));
-            }
-        }
+        };
 
         if (!WRITE) {
-            if (active) {
-                a.cnt[tbeg + kk] = found;
-                if (a.counts_user) a.counts_user[caller] = found;
+            // ---------------- count pass
+            uint16_t* lb = s_lb[threadIdx.x];
+            const bool slots = one_chunk && a.slot != nullptr;
+            uint16_t* myslot = a.slot + (size_t)j * a.K;
+            for (int c = 0; c < nchunks; ++c) {
+                ensure_chunk(c);
+                if (!active) continue;
+                if (slots) {
+                    sweep(c, [&](int v, int k) {
+                        if (k < a.K) {
+                            lb[k & 7] = (uint16_t)v;
+                            if ((k & 7) == 7) *(uint4*)(myslot + (k - 7)) = *(const uint4*)lb;
+                        }
+                    });
+                } else {
+                    sweep(c, [&](int, int) {});
+                }
             }
-            int64_t bt;
-            block_excl_scan<int64_t, kBlock>((int64_t)found, sh.w64, &bt);
-            tile_edges += bt;
-        } else {
-            ebase += btot;  // the next batch starts after this batch's edges
+            if (active) {
+                if (slots && (found & 7) && found < a.K)
+                    *(uint4*)(myslot + (found & ~7)) = *(const uint4*)lb;
+                a.cnt[j] = found;
+                if (a.counts_user) a.counts_user[caller] = found;
+                tile_found += found;
+            }
+            __syncthreads();
+            continue;
         }
+
+        // ---------------- write pass
+        const int mycnt = active ? a.cnt[j] : 0;
+        int btot;
+        const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
+        if (active) {
+            sh.off[threadIdx.x] = ex;
+            sh.tid[threadIdx.x] = my_id;
+            sh.tf[threadIdx.x] = my_f;
+        }
+        if (threadIdx.x == 0) sh.off[nbatch] = btot;
+        __syncthreads();  // offsets / target tables visible to the whole workgroup
+        if (one_chunk) {
+            ensure_chunk(0);
+            // every edge of the batch: (target, k) from the offsets, neighbour from the slot
+            for (int e = threadIdx.x; e < btot; e += kBlock) {
+                int lo = 0, hi = nbatch;
+                while (hi - lo > 1) {
+                    const int mid = (lo + hi) >> 1;
+                    if (sh.off[mid] <= e) lo = mid; else hi = mid;
+                }
+                const int k = e - sh.off[lo];
+                if (k >= a.K) continue;  // written by the sweep below
+                const int v = min((int)a.slot[(size_t)(tbeg + k0 + lo) * a.K + k], kCap);
+                const uint32_t Tp = sh.T[v];
+                const uint32_t ft = sh.tf[lo];
+                emit_edge(a, ebase + e, __float_as_int(sh.q[v].w), sh.tid[lo],
+                          unpack3(Tp, 0) + unpack3(ft, 0), unpack3(Tp, 1) + unpack3(ft, 1),
+                          unpack3(Tp, 2) + unpack3(ft, 2));
+            }
+            // targets with more than K neighbours: the rest by a second sweep
+            const bool over = active && mycnt > a.K;
+            if (__syncthreads_or(over)) {
+                if (over) {
+                    const int64_t base = ebase + ex;
+                    sweep(0, [&](int v, int k) {
+                        if (k >= a.K && k < mycnt) {
+                            const uint32_t Tp = sh.T[v];
+                            emit_edge(a, base + k, __float_as_int(sh.q[v].w), my_id,
+                                      unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
+                        }
+                    });
+                }
+            }
+        } else {
+            // chunked region (very dense tiles): sweep and write directly
+            const int64_t base = ebase + ex;
+            for (int c = 0; c < nchunks; ++c) {
+                ensure_chunk(c);
+                if (!active) continue;
+                sweep(c, [&](int v, int k) {
+                    if (k < mycnt) {
+                        const uint32_t Tp = sh.T[v];
+                        emit_edge(a, base + k, __float_as_int(sh.q[v].w), my_id,
+                                  unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
+                    }
+                });
+            }
+        }
+        ebase += btot;
         __syncthreads();
-        k0 += nbatch;
     }
-    if (!WRITE && threadIdx.x == 0) a.ttot[rank] = (int)tile_edges;
+
+    if (!WRITE) {
+        int64_t tt;
+        block_excl_scan<int64_t, kBlock>(tile_found, sh.w64, &tt);
+        if (threadIdx.x == 0) a.ttot[rank] = (int)tt;
+    }
 }
 
 // ---------------------------------------------------------------- all-pairs fallback
@@ -816,7 +847,19 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     SearchArgs a;
     memset(&a, 0, sizeof a);
     memcpy(a.C, p.C, sizeof a.C);
+    for (int d = 0; d < 3; ++d)
+        for (int c = 0; c < 3; ++c) a.hC[3 * d + c] = p.C[3 * d + c] / (double)p.nb[d];
     a.r2 = p.r2;
+    a.ortho = p.C[1] == 0.0 && p.C[2] == 0.0 && p.C[3] == 0.0 && p.C[5] == 0.0 && p.C[6] == 0.0 &&
+              p.C[7] == 0.0 && p.C[0] > 0.0 && p.C[4] > 0.0 && p.C[8] > 0.0;
+    for (int d = 0; d < 3; ++d) {
+        a.hb[d] = (float)(p.C[4 * d] / p.nb[d]);
+        a.hbinv[d] = (float)(p.nb[d] / p.C[4 * d]);
+    }
+    // row trimming must never drop a candidate the exact test could accept: pad the
+    // cutoff by far more than the fp32 position error
+    a.pmargin = (float)(1e-4 * p.r + 1e-3);
+    a.rprune2 = (float)((p.r + 2.0 * a.pmargin) * (p.r + 2.0 * a.pmargin));
     for (int d = 0; d < 3; ++d) {
         a.nb[d] = p.nb[d]; a.P[d] = p.P[d]; a.T[d] = p.T[d]; a.ntl[d] = p.ntl[d];
         a.R[d] = p.R[d]; a.pbc[d] = p.pbc[d];
@@ -840,6 +883,8 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.ttot = at<int>(ws, p.o_ttot);
     a.tbase = at<int64_t>(ws, p.o_tbase);
     a.totals = at<int64_t>(ws, p.o_tot);
+    a.slot = at<uint16_t>(ws, p.o_slot);
+    a.K = p.K;
     return a;
 }
 
@@ -948,7 +993,7 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
     // 6. degrees
     SearchArgs a = search_args(p, pos, ws);
     a.counts_user = counts_out;
-    hipLaunchKernelGGL(search_kernel<false>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(search_kernel<0>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
     // 7. tile offsets in SFC order
     device_excl_scan<int, int64_t>(at<int>(ws, p.o_ttot), p.ntiles, at<int64_t>(ws, p.o_tbase),
                                    at<int64_t>(ws, p.o_part), s);
@@ -1006,7 +1051,7 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
     a.out_src = edge_src; a.out_dst = edge_dst; a.out_shift = cell_shift;
     a.out_vec = edge_vec; a.out_dist = edge_dist; a.vout_f64 = vec_dtype == DG_F64;
     a.capacity = capacity;
-    hipLaunchKernelGGL(search_kernel<true>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(search_kernel<1>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
     return check_launch("dg_graph_write");
 }
 

@@ -18,8 +18,8 @@
 namespace dg {
 
 constexpr int kBlock = 256;      // threads per search workgroup (4 x wave64)
-constexpr int kMaxRegion = 512;  // region bins staged per tile
-constexpr int kTileEdge = 4;     // target bins per tile edge (4x4x4)
+constexpr int kMaxRegion = 768;  // region bins staged per tile
+constexpr int kTileTargets = 235; // aim: targets per tile <= this (a 256-lane workgroup)
 
 struct Plan {
     int64_t n = 0, nt = 0;  // atoms, targets
@@ -40,7 +40,8 @@ struct Plan {
     size_t o_key, o_rank, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
     size_t o_cflag, o_cpos, o_tor, o_rot;
     size_t o_tkey, o_trank, o_tbcnt, o_tbstart, o_tslot, o_tsidx, o_tcaller;
-    size_t o_cnt, o_ttot, o_tbase, o_part, o_tot;
+    size_t o_cnt, o_ttot, o_tbase, o_part, o_tot, o_slot;
+    int K = 0;              // neighbour slot entries per target
     size_t ws_bytes = 0;
 };
 
@@ -93,18 +94,29 @@ inline void plan_grid(Plan& p)
         p.nb[d] = (int)nbd[d];
         p.P[d] = (int)ceil(p.cf[d] * p.nb[d] * (1.0 + 1e-9) + 1e-12);
         if (p.P[d] < 1) p.P[d] = 1;
-        p.T[d] = std::min(kTileEdge, p.nb[d]);
+    }
+    // Tile: as many bins as keep the expected targets of a tile within one 256-lane
+    // workgroup, with a region of at most kMaxRegion bins; prefer compact tiles.
+    {
+        const double per_bin = (double)std::max<int64_t>(p.subset ? p.nt : p.n, 1) /
+                               ((double)p.nb[0] * p.nb[1] * p.nb[2]);
+        int best[3] = {1, 1, 1};
+        double best_score = -1;
+        for (int a = 1; a <= std::min(6, p.nb[0]); ++a)
+            for (int b = 1; b <= std::min(6, p.nb[1]); ++b)
+                for (int c = 1; c <= std::min(6, p.nb[2]); ++c) {
+                    const int64_t reg = (int64_t)(a + 2 * p.P[0]) * (b + 2 * p.P[1]) * (c + 2 * p.P[2]);
+                    if (reg > kMaxRegion) continue;
+                    if (a * b * c * per_bin > kTileTargets && a * b * c > 1) continue;
+                    // most bins per tile first, then the least halo per bin
+                    const double score = a * b * c * 1e6 - (double)reg / (a * b * c);
+                    if (score > best_score) { best_score = score; best[0] = a; best[1] = b; best[2] = c; }
+                }
+        for (int d = 0; d < 3; d++) p.T[d] = best[d];
     }
     auto region = [&]() {
         return (int64_t)(p.T[0] + 2 * p.P[0]) * (p.T[1] + 2 * p.P[1]) * (p.T[2] + 2 * p.P[2]);
     };
-    while (region() > kMaxRegion) {
-        int best = -1;
-        for (int d = 0; d < 3; d++)
-            if (p.T[d] > 1 && (best < 0 || p.T[d] + 2 * p.P[d] > p.T[best] + 2 * p.P[best])) best = d;
-        if (best < 0) break;
-        p.T[best]--;
-    }
     p.brute = region() > kMaxRegion;
     for (int d = 0; d < 3; d++) {
         p.R[d] = p.T[d] + 2 * p.P[d];
@@ -139,6 +151,16 @@ inline void plan_grid(Plan& p)
     p.lo_in = lo > 0 ? nextafterf((float)lo, 0.0f) : 0.0f;
     double t = sqrt(kSelfThr) + 2.0 * sqrt(3.0) * delta;
     p.tiny = nextafterf((float)(t * t * (1.0 + 1e-3)), INFINITY);
+
+    // Neighbour slot per target: the expected degree at the mean density with ample
+    // headroom (targets past it are swept a second time in the write pass).
+    const double vol = fabs(p.C[0] * (p.C[4] * p.C[8] - p.C[5] * p.C[7]) -
+                            p.C[1] * (p.C[3] * p.C[8] - p.C[5] * p.C[6]) +
+                            p.C[2] * (p.C[3] * p.C[7] - p.C[4] * p.C[6]));
+    const double deg = (double)p.n / vol * (4.0 / 3.0) * 3.14159265358979 * p.r * p.r * p.r;
+    double k = 1.3 * deg + 32.0;
+    k = std::min(std::max(k, 32.0), 2048.0);
+    p.K = ((int)k + 7) & ~7;
 }
 
 inline void plan_layout(Plan& p)
@@ -168,6 +190,7 @@ inline void plan_layout(Plan& p)
     p.o_tsidx = take(p.subset ? 4 * nt : 0);
     p.o_tcaller = take(p.subset ? 4 * nt : 0);
     p.o_cnt = take(4 * nt);
+    p.o_slot = take(2 * (size_t)p.K * nt);
     p.o_ttot = take(4 * std::max(ntl, nt));
     p.o_tbase = take(8 * (std::max(ntl, nt) + 1));
     // scan partials: one int64 per 2048-item block of the largest scan
