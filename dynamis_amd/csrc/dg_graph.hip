@@ -49,6 +49,10 @@ constexpr int kCap = 1792;    // region entries staged in LDS per chunk
 constexpr int kRegPerThread = (kMaxRegion + kBlock - 1) / kBlock;
 constexpr int kBinSortMax = 128;
 
+// Value known to be uniform across the wave, moved to a scalar register.
+__device__ __forceinline__ int rfl(int x) { return __builtin_amdgcn_readfirstlane(x); }
+__device__ __forceinline__ uint32_t rfl(uint32_t x) { return (uint32_t)__builtin_amdgcn_readfirstlane((int)x); }
+
 __device__ __forceinline__ void load_pos(const void* pos, int f64, int64_t i, double* p)
 {
     if (f64) {
@@ -553,19 +557,25 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
                     const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
                     const int va = max(sh.rp[rb + xlo], c0) - c0;
                     const int vb = min(sh.rp[rb + xhi + 1], c1) - c0;
-                    for (int v = va; v < vb; ++v) {
-                        const float4 q = sh.q[v];
-                        const float dx = q.x - t0, dyv = q.y - t1, dzv = q.z - t2;
-                        const float d2 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
-                        bool edge = d2 < a.lo_in && d2 > a.tiny;
-                        if (__builtin_expect(!edge && d2 <= a.hi && v != vs, false)) {
-                            const uint32_t Tp = sh.T[v];
-                            edge = exact_edge(a, __float_as_int(q.w), my_id, unpack3(Tp, 0) + fx,
-                                              unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
-                        }
-                        if (edge) {
-                            on_edge(v, found);
-                            ++found;
+                    if (va < vb) {
+                        // the next candidate's load is issued before this one is tested
+                        float4 qn = sh.q[va];
+                        for (int v = va; v < vb; ++v) {
+                            const float4 q = qn;
+                            qn = sh.q[min(v + 1, vb - 1)];
+                            const float dx = q.x - t0, dyv = q.y - t1, dzv = q.z - t2;
+                            const float d2 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
+                            bool edge = d2 < a.lo_in && d2 > a.tiny;
+                            const bool band = !edge && d2 <= a.hi && v != vs;
+                            if (__builtin_expect(band, false)) {
+                                const uint32_t Tp = sh.T[v];
+                                edge = exact_edge(a, __float_as_int(q.w), my_id, unpack3(Tp, 0) + fx,
+                                                  unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
+                            }
+                            if (edge) {
+                                on_edge(v, found);
+                                ++found;
+                            }
                         }
                     }
                 }
@@ -615,21 +625,57 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
         __syncthreads();  // offsets / target tables visible to the whole workgroup
         if (one_chunk) {
             ensure_chunk(0);
-            // every edge of the batch: (target, k) from the offsets, neighbour from the slot
-            for (int e = threadIdx.x; e < btot; e += kBlock) {
-                int lo = 0, hi = nbatch;
-                while (hi - lo > 1) {
-                    const int mid = (lo + hi) >> 1;
-                    if (sh.off[mid] <= e) lo = mid; else hi = mid;
+            // The batch's edges are split evenly over the waves; each wave walks its range
+            // 64 edges at a time, lane e finding its target by a short forward walk from the
+            // wave's current target (a 64-edge chunk spans one or two targets).  Stores use
+            // 32-bit offsets from the wave's bases and are fully coalesced.
+            {
+                const int lane = threadIdx.x & 63;
+                const int w = threadIdx.x >> 6;
+                const int NWv = kBlock / 64;
+                const bool plain = !a.out_vec && !a.out_dist;
+                const int E0 = (int)(((int64_t)btot * w) / NWv), E1 = (int)(((int64_t)btot * (w + 1)) / NWv);
+                int tcur = 0;
+                {
+                    int lo = 0, hi = nbatch;  // target containing E0
+                    while (hi - lo > 1) {
+                        const int mid = (lo + hi) >> 1;
+                        if (sh.off[mid] <= E0) lo = mid; else hi = mid;
+                    }
+                    tcur = rfl(lo);
                 }
-                const int k = e - sh.off[lo];
-                if (k >= a.K) continue;  // written by the sweep below
-                const int v = min((int)a.slot[(size_t)(tbeg + k0 + lo) * a.K + k], kCap);
-                const uint32_t Tp = sh.T[v];
-                const uint32_t ft = sh.tf[lo];
-                emit_edge(a, ebase + e, __float_as_int(sh.q[v].w), sh.tid[lo],
-                          unpack3(Tp, 0) + unpack3(ft, 0), unpack3(Tp, 1) + unpack3(ft, 1),
-                          unpack3(Tp, 2) + unpack3(ft, 2));
+                const int64_t wbase = ebase + E0;
+                int64_t* __restrict__ ps = a.out_src + wbase;
+                int64_t* __restrict__ pd = a.out_dst + wbase;
+                float* __restrict__ pf = a.out_shift + 3 * wbase;
+                const uint16_t* __restrict__ sl = a.slot + (size_t)(tbeg + k0) * a.K;
+                for (int e0 = E0; e0 < E1; e0 += 64) {
+                    const int e = e0 + lane;
+                    int t = tcur;
+                    if (e < E1) {
+                        while (sh.off[t + 1] <= e) ++t;
+                        const int k = e - sh.off[t];
+                        if (k < a.K) {
+                            const int vk = min((int)sl[(uint32_t)(t * a.K + k)], kCap);
+                            const uint32_t Tp = sh.T[vk];
+                            const uint32_t ft = sh.tf[t];
+                            const int src = __float_as_int(sh.q[vk].w);
+                            const int S0 = unpack3(Tp, 0) + unpack3(ft, 0);
+                            const int S1 = unpack3(Tp, 1) + unpack3(ft, 1);
+                            const int S2 = unpack3(Tp, 2) + unpack3(ft, 2);
+                            const uint32_t r = (uint32_t)(e - E0);
+                            if (plain) {
+                                ps[r] = src;
+                                pd[r] = sh.tid[t];
+                                *(float3*)(pf + 3 * r) = make_float3((float)S0, (float)S1, (float)S2);
+                            } else {
+                                emit_edge(a, wbase + r, src, sh.tid[t], S0, S1, S2);
+                            }
+                        }
+                    }
+                    // next chunk starts in the target of this chunk's last edge
+                    tcur = __builtin_amdgcn_readlane(t, min(63, E1 - e0 - 1));
+                }
             }
             // targets with more than K neighbours: the rest by a second sweep
             const bool over = active && mycnt > a.K;
