@@ -6,7 +6,7 @@ of the 1M-atom, r_cut = 6 A uniform box (config C3) on one MI355X.
 One step = one full rebuild through the C ABI (dg_graph_count + dg_graph_write) into
 preallocated output buffers, positions already resident in HBM, no host sync inside the
 step.  Prints ONE JSON line.  `roofline` is for the dominant kernel (the edge-write search
-pass, search_kernel<true>, the only kernel dg_graph_write launches), timed with HIP events
+pass, search_kernel<1>, the only kernel dg_graph_write launches), timed with HIP events
 on the stream it runs on.  `cpu_baseline` times the CPU oracle (a restatement of the
 reference algorithm) on the same box on this host.
 """
@@ -35,7 +35,20 @@ def main():
     ap.add_argument("--config", default="C3")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--copy-calibration", action="store_true",
+                    help="run only a plain 1 GiB device-to-device copy (5 times): the reference "
+                         "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
     args = ap.parse_args()
+    if args.copy_calibration:
+        import torch
+
+        src = torch.empty(1 << 30, dtype=torch.uint8, device="cuda:0").fill_(1)
+        dst = torch.empty_like(src)
+        for _ in range(5):
+            dst.copy_(src)
+        torch.cuda.synchronize()
+        print(json.dumps({"copy_calibration_bytes": 1 << 30, "repeats": 5}))
+        return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
               "graph build shards by space with no collective inside it -- see DESIGN.md.",
@@ -138,12 +151,15 @@ def main():
     kbytes = WRITE_BYTES_PER_EDGE * E + 20 * n + 4 * nt
     achieved = kbytes / (write_ms * 1e-3) / 1e9
 
+    # HBM bytes per launch of the write kernel measured by rocprofv3 (FETCH_SIZE +
+    # WRITE_SIZE, scaled by a plain copy of known size); recorded in profiles/ by the
+    # commands written there, for this config.
     traffic = None
     tfile = os.path.join(ROOT, "profiles", f"search_write_{args.config}_traffic.json")
     if os.path.exists(tfile):
         try:
             traffic = json.load(open(tfile)).get("bytes_per_launch")
-        except Exception:
+        except (OSError, ValueError):
             traffic = None
 
     cpu = None
@@ -189,7 +205,7 @@ def main():
         "api_ms_per_rebuild": round(api_ms, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "search_kernel<true> (edge write)",
+                     "kernel": "search_kernel<1> (edge write)",
                      "algorithmic_bytes": kbytes},
         "cpu_baseline": cpu,
     }
