@@ -14,7 +14,7 @@ import torch  # noqa: F401  (must precede the dlopen below)
 _HERE = os.path.dirname(os.path.abspath(__file__))
 LIB_PATH = os.path.join(_HERE, "libdynamis_graph.so")
 
-DG_F32, DG_F64, DG_I64 = 0, 1, 2
+DG_F32, DG_F64, DG_I64, DG_I32 = 0, 1, 2, 3
 DG_OK, DG_ERR_INVALID, DG_ERR_WORKSPACE, DG_ERR_HIP, DG_ERR_RANGE, DG_ERR_CAPACITY = range(6)
 
 
@@ -30,6 +30,20 @@ class GraphDesc(ctypes.Structure):
         ("pbc", ctypes.c_uint8 * 3),
         ("pad_", ctypes.c_uint8 * 5),
         ("radius", ctypes.c_double),
+    ]
+
+
+class HaloDesc(ctypes.Structure):
+    """dg_halo_desc."""
+
+    _fields_ = [
+        ("n_atoms", ctypes.c_int64),
+        ("n_edges", ctypes.c_int64),
+        ("num_local", ctypes.c_int64),
+        ("my_rank", ctypes.c_int64),
+        ("world_size", ctypes.c_int64),
+        ("pid_dtype", ctypes.c_int32),
+        ("pad_", ctypes.c_int32),
     ]
 
 
@@ -63,6 +77,10 @@ def lib():
         "dg_sfc_keys": (_i32, [_p, _i64, _i32, _p, _p, _sz, _p]),
         "dg_sfc_order": (_i32, [_p, _i64, _p, _p, _sz, _p]),
         "dg_sfc_labels": (_i32, [_p, _i64, _i64, _p, _p, _p, _sz, _p]),
+        "dg_halo_workspace_size": (_sz, [_i64, _i64]),
+        "dg_halo_count": (_i32, [ctypes.POINTER(HaloDesc), _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
+        "dg_halo_read_totals": (_i32, [_p, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _p]),
+        "dg_halo_write": (_i32, [ctypes.POINTER(HaloDesc), _p, _p, _p, _p, _p, _sz, _p]),
         "dg_last_error": (ctypes.c_char_p, []),
         "dg_version": (ctypes.c_char_p, []),
     }

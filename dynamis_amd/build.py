@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libdynamis_graph.so")
-SOURCES = ["dg_graph.hip", "dg_sfc.hip"]
+SOURCES = ["dg_graph.hip", "dg_sfc.hip", "dg_halo.hip"]
 ARCH = os.environ.get("DG_OFFLOAD_ARCH", "gfx950")
 
 HIPCC = os.environ.get("HIPCC", "/opt/rocm/bin/hipcc")

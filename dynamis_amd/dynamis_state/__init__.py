@@ -9,5 +9,8 @@ Mirrors dynamis_state/src/dynamis_state/__init__.py:17 (``radius_graph_pbc_cuda`
 from . import dynamis_state_impl
 from .dynamis_state_impl import SFCCurveType
 from .radius_graph_pbc_cuda import radius_graph_pbc_cuda
+from . import dist_graph_builder
+from .dist_graph_builder import BuildMode, DistBuildGraphResult, DistGraphBuilder
 
-__all__ = ["dynamis_state_impl", "radius_graph_pbc_cuda", "SFCCurveType"]
+__all__ = ["dynamis_state_impl", "radius_graph_pbc_cuda", "SFCCurveType", "dist_graph_builder",
+           "DistGraphBuilder", "DistBuildGraphResult", "BuildMode"]

@@ -1,0 +1,245 @@
+"""Per-rank graph builder with a graph-aware halo, on the gfx950 graph kernels.
+
+Mirror of dynamis_state/src/dynamis_state/dist_graph_builder.py:234-495 (same class,
+arguments, result fields and mode schedule).  Every rank holds the full position array;
+each rank builds only the edges whose target it owns.
+
+Refresh (mode A, every ``refresh_interval`` calls, or early when an atom drifted more
+than ``drift_threshold`` since the last refresh):
+  1. wrap positions into the orthorhombic box;
+  2. block-partition a uniform grid of cells of side >= r + skin over the ranks;
+  3. r-degrees of the atoms in my cells (radius_graph_pbc_counts_ex, no edge list);
+  4. sum the degrees over ranks (one all_reduce of 4 B/atom);
+  5. SFC partition weighted by degree -> pid_outer, my_outer_atoms;
+  6. edges at r + skin for my_outer targets (radius_graph_pbc_ex);
+  7. halo plan from those edges (extract_halo_info; no exchange of plans: the graph is
+     symmetric, so what I receive from p is what p computes it sends to me);
+  8. the output edges: step 6's edges filtered to r (filter_edges_to_radius).
+Steady (mode B): edges at r over my_outer + the cached halo, targets = my_outer, mapped
+back to global ids.  No collective.
+
+The only collective is the degree sum.  With the gloo backend it runs on a host copy
+(gloo is given CPU tensors only); with nccl (RCCL) on the device tensor.
+"""
+from __future__ import annotations
+
+from dataclasses import dataclass
+from enum import Enum
+from typing import Optional, Tuple
+
+import torch
+import torch.distributed as dist
+
+from . import dynamis_state_impl as _impl
+
+
+class BuildMode(Enum):
+    REFRESH = "A"
+    STEADY = "B"
+
+
+@dataclass
+class DistBuildGraphResult:
+    """One build's output (dist_graph_builder.py:44-59)."""
+
+    edges_outer: torch.Tensor          # [2, E_local] global ids, dst in my_outer
+    cell_shifts_outer: torch.Tensor    # [E_local, 3] float32
+    pid_outer: torch.Tensor            # [N] int64 owner rank
+    my_outer_atoms: torch.Tensor       # [num_local] int64 global ids, ascending
+    halo_info: _impl.PartitionMessagePassingInfo
+    interior_mask: torch.Tensor        # [num_local] bool
+    full_degrees: torch.Tensor         # [N] int32 r-degrees of the last refresh
+    halo_recv_global_ids: torch.Tensor  # [total_recv] int64, by peer then id
+    mode: BuildMode
+
+
+def _cell_block_partition(pos_w: torch.Tensor, L_vec: torch.Tensor, cell_size: float,
+                          rank: int, world_size: int) -> torch.Tensor:
+    """Atoms of the cells owned by ``rank`` (dist_graph_builder.py:67-111): a grid of
+    floor(L / cell_size) cells per axis (at least 1) covering the box exactly, linear
+    cell id x-fastest, rank r owning ids [r * n / W, (r + 1) * n / W)."""
+    L_vec = L_vec.to(pos_w.device)
+    nc = [max(1, int(torch.floor(L_vec[d] / cell_size).item())) for d in range(3)]
+    cid = torch.zeros(pos_w.shape[0], dtype=torch.int64, device=pos_w.device)
+    stride = 1
+    for d in range(3):
+        size = L_vec[d] / nc[d]
+        c = torch.clamp(torch.floor(pos_w[:, d] / size).to(torch.int64), 0, nc[d] - 1)
+        cid += c * stride
+        stride *= nc[d]
+    n = stride
+    lo, hi = (rank * n) // world_size, ((rank + 1) * n) // world_size
+    return torch.nonzero((cid >= lo) & (cid < hi), as_tuple=False).squeeze(-1)
+
+
+def _all_reduce_degrees(degrees_local: torch.Tensor, my_target_atoms: torch.Tensor, N: int,
+                        group=None) -> torch.Tensor:
+    """[N] int32 degrees, my entries scattered in, summed over ranks (:114-125)."""
+    full = torch.zeros(N, dtype=torch.int32, device=degrees_local.device)
+    if degrees_local.numel() > 0:
+        full.scatter_(0, my_target_atoms.to(torch.int64), degrees_local.to(torch.int32))
+    if dist.is_available() and dist.is_initialized():
+        if dist.get_backend(group) == "gloo":
+            host = full.cpu()
+            dist.all_reduce(host, op=dist.ReduceOp.SUM, group=group)
+            full.copy_(host)
+        else:
+            dist.all_reduce(full, op=dist.ReduceOp.SUM, group=group)
+    return full
+
+
+def _compute_sfc_weighted_partition(pos: torch.Tensor, full_degrees: torch.Tensor,
+                                    env: _impl.DistEnvironment,
+                                    curve_type=_impl.SFCCurveType.Morton) -> torch.Tensor:
+    """pid [N] int64 from the degree-weighted SFC cut (:128-146)."""
+    mol = _impl.MolecularInfo()
+    mol.num_atoms = pos.shape[0]
+    mol.atom_positions = pos.contiguous()
+    mol.atom_vertex_numbers = torch.arange(pos.shape[0], dtype=torch.int64, device=pos.device)
+    mol.edge_counts = full_degrees.to(torch.int64).contiguous()
+    return _impl.SFCPartitioner(curve_type).partition(mol, env).partition_id
+
+
+def _extract_halo_info_local(edges, pid_outer, my_outer_atoms, my_rank, world_size, N, device
+                             ) -> Tuple[_impl.PartitionMessagePassingInfo, torch.Tensor, torch.Tensor]:
+    """Step 7 (:149-203): (halo_info, interior_mask, halo_recv_global_ids)."""
+    so, sl, ro, rg, interior, recv_atom = _impl.extract_halo_info(
+        edges, pid_outer, my_outer_atoms, my_rank, world_size, N)
+    info = _impl.PartitionMessagePassingInfo()
+    info.partition_id = pid_outer
+    info.partition_indices = my_outer_atoms
+    info.global_send_recv_matrix = torch.zeros(world_size, world_size, dtype=torch.int64,
+                                               device=device)
+    info.send_offsets = so
+    info.send_local_indices = sl
+    info.recv_offsets = ro
+    info.recv_ghost_indices = rg
+    info.interior_mask = interior
+    return info, interior, recv_atom
+
+
+def _filter_edges_to_radius(edges, cell_shifts, pos, cell, r):
+    """Step 8 (:206-227).  r is rounded to float32 as the graph build rounds its radius,
+    so filtering the r + skin graph to r gives exactly the graph at r."""
+    if edges.numel() == 0:
+        return edges, cell_shifts
+    return _impl.filter_edges_to_radius(edges, cell_shifts, pos, cell, _impl._r32(r))
+
+
+class DistGraphBuilder:
+    """dist_graph_builder.py:234-495; see the module docstring for the two modes.
+
+    Args: cell [3,3] (orthorhombic: the box lengths are its diagonal), pbc [3], cutoff r,
+    ghost_buffer (skin), env (DistEnvironment), refresh_interval K, max_num_neighbors and
+    enforce_max_strictly (validated and passed through, as the reference), drift_threshold
+    (default skin / 2), process_group, sfc_curve_type, partition_cell_size (default r + skin).
+    """
+
+    def __init__(self, cell, pbc, cutoff: float, ghost_buffer: float, env,
+                 refresh_interval: int = 100, max_num_neighbors: int = 0,
+                 enforce_max_strictly: bool = False, drift_threshold: Optional[float] = None,
+                 process_group=None, sfc_curve_type=_impl.SFCCurveType.Morton,
+                 partition_cell_size: Optional[float] = None):
+        self.cell = cell
+        self.pbc = pbc
+        self.cutoff = float(cutoff)
+        self.ghost_buffer = float(ghost_buffer)
+        self.r_plus_skin = self.cutoff + self.ghost_buffer
+        self.env = env
+        self.refresh_interval = int(refresh_interval)
+        self.max_num_neighbors = int(max_num_neighbors)
+        self.enforce_max_strictly = bool(enforce_max_strictly)
+        self.drift_threshold = (float(drift_threshold) if drift_threshold is not None
+                                else self.ghost_buffer / 2.0)
+        self.process_group = process_group
+        self.sfc_curve_type = sfc_curve_type
+        self.partition_cell_size = (float(partition_cell_size) if partition_cell_size is not None
+                                    else self.r_plus_skin)
+        self._L_vec = torch.as_tensor(cell).diag().contiguous()
+        self.reset()
+
+    @property
+    def next_is_refresh(self) -> bool:
+        return self._steps_since_refresh >= self.refresh_interval
+
+    def reset(self) -> None:
+        self._pid_outer = None
+        self._my_outer_atoms = None
+        self._halo_recv_global_ids = None
+        self._halo_info = None
+        self._interior_mask = None
+        self._full_degrees = None
+        self._pos_w_at_refresh = None
+        self._steps_since_refresh = self.refresh_interval  # first call refreshes
+
+    def _pbc_wrap(self, pos: torch.Tensor) -> torch.Tensor:
+        L = self._L_vec.to(pos.device, pos.dtype).unsqueeze(0)
+        return pos - torch.floor(pos / L) * L
+
+    def _live_drift_exceeded(self, pos_w: torch.Tensor) -> bool:
+        """Largest minimum-image displacement since the refresh > drift_threshold."""
+        if self._pos_w_at_refresh is None:
+            return False
+        L = self._L_vec.to(pos_w.device, pos_w.dtype).unsqueeze(0)
+        dlt = (pos_w - self._pos_w_at_refresh).abs()
+        dlt = torch.minimum(dlt, L - dlt)
+        return float(dlt.max().item()) > self.drift_threshold
+
+    def _mode_a(self, pos: torch.Tensor) -> DistBuildGraphResult:
+        R, W = int(self.env.global_rank), int(self.env.world_size)
+        dev = pos.device
+        N = pos.shape[0]
+        pbc = torch.as_tensor(self.pbc)
+        cell = torch.as_tensor(self.cell).to(dev, pos.dtype)
+        pos_w = self._pbc_wrap(pos)
+        mine_cells = _cell_block_partition(pos_w, self._L_vec.to(dev), self.partition_cell_size, R, W)
+        if mine_cells.numel() > 0:
+            deg_local = _impl.radius_graph_pbc_counts_ex(pos_w, cell, pbc, self.cutoff, mine_cells)
+        else:
+            deg_local = torch.empty(0, dtype=torch.int32, device=dev)
+        full_degrees = _all_reduce_degrees(deg_local, mine_cells, N, group=self.process_group)
+        pid = _compute_sfc_weighted_partition(pos_w, full_degrees, self.env, self.sfc_curve_type)
+        my_outer = torch.nonzero(pid.eq(R), as_tuple=False).squeeze(-1)
+        e_skin, s_skin, _, _ = _impl.radius_graph_pbc_ex(
+            pos_w, cell, pbc, self.r_plus_skin, self.max_num_neighbors, self.enforce_max_strictly,
+            my_outer)
+        halo_info, interior, recv_ids = _extract_halo_info_local(e_skin, pid, my_outer, R, W, N, dev)
+        edges, shifts = _filter_edges_to_radius(e_skin, s_skin, pos_w, cell, self.cutoff)
+        self._pid_outer = pid
+        self._my_outer_atoms = my_outer
+        self._halo_recv_global_ids = recv_ids
+        self._halo_info = halo_info
+        self._interior_mask = interior
+        self._full_degrees = full_degrees
+        self._pos_w_at_refresh = pos_w.detach().clone()
+        self._steps_since_refresh = 0
+        return DistBuildGraphResult(edges, shifts, pid, my_outer, halo_info, interior,
+                                    full_degrees, recv_ids, BuildMode.REFRESH)
+
+    def _mode_b(self, pos: torch.Tensor) -> DistBuildGraphResult:
+        dev = pos.device
+        pbc = torch.as_tensor(self.pbc)
+        cell = torch.as_tensor(self.cell).to(dev, pos.dtype)
+        pos_w = self._pbc_wrap(pos)
+        if self._live_drift_exceeded(pos_w):
+            self._steps_since_refresh = self.refresh_interval
+            return self._mode_a(pos)
+        ids = torch.cat([self._my_outer_atoms, self._halo_recv_global_ids])
+        local_pos = pos_w.index_select(0, ids).contiguous()
+        targets = torch.arange(self._my_outer_atoms.numel(), dtype=torch.int64, device=dev)
+        e_loc, shifts, _, _ = _impl.radius_graph_pbc_ex(
+            local_pos, cell, pbc, self.cutoff, self.max_num_neighbors, self.enforce_max_strictly,
+            targets)
+        if e_loc.numel() == 0:
+            edges = torch.empty(2, 0, dtype=torch.int64, device=dev)
+        else:
+            edges = ids[e_loc.reshape(-1)].reshape(2, -1)
+        self._steps_since_refresh += 1
+        return DistBuildGraphResult(edges, shifts, self._pid_outer, self._my_outer_atoms,
+                                    self._halo_info, self._interior_mask, self._full_degrees,
+                                    self._halo_recv_global_ids, BuildMode.STEADY)
+
+    def build(self, pos: torch.Tensor) -> DistBuildGraphResult:
+        if self.next_is_refresh or self._halo_info is None:
+            return self._mode_a(pos)
+        return self._mode_b(pos)

@@ -244,6 +244,63 @@ def filter_edges_to_radius(edges, cell_shifts, pos, cell, radius):
         return edges.index_select(1, idx).contiguous(), cell_shifts.index_select(0, idx).contiguous()
 
 
+def extract_halo_info(edges, pid_outer, my_outer_atoms, my_rank, world_size, N):
+    """Halo send/recv CSR and interior mask of one rank from its edges (every dst in
+    ``my_outer_atoms``), dist_graph_ops.cpp:38-60 / dist_graph_ops_kernels.cu:104-188.
+
+    Returns (send_offsets [W+1] int64, send_local_indices int64 (positions into
+    my_outer_atoms), recv_offsets [W+1] int64, recv_ghost_indices int64
+    (arange(num_local, num_local + total_recv)), interior_mask [num_local] bool,
+    recv_atom_global int64), both lists grouped by peer rank and sorted by global atom id
+    inside a peer.  One host sync (the list sizes).
+    """
+    _check(isinstance(edges, torch.Tensor) and edges.is_cuda, "edges must be a CUDA tensor")
+    _check(edges.dim() == 2 and edges.size(0) == 2,
+           f"edges must have shape [2, E], got {list(edges.shape)}")
+    _check(edges.dtype == torch.int64, "edges must be int64")
+    N = int(N)
+    _check(isinstance(pid_outer, torch.Tensor) and pid_outer.is_cuda and pid_outer.dim() == 1,
+           "pid_outer must be a 1-D CUDA tensor")
+    _check(pid_outer.size(0) == N, f"pid_outer must have length N ({N}), got {pid_outer.size(0)}")
+    _check(isinstance(my_outer_atoms, torch.Tensor) and my_outer_atoms.is_cuda
+           and my_outer_atoms.dim() == 1 and my_outer_atoms.dtype == torch.int64,
+           "my_outer_atoms must be 1-D int64 CUDA")
+    W, R = int(world_size), int(my_rank)
+    _check(W >= 1, f"world_size must be >= 1, got {W}")
+    _check(0 <= R < W, "my_rank must be in [0, world_size)")
+    lib = L.lib()
+    dev = edges.device
+    edges = edges.contiguous()
+    if pid_outer.dtype not in (torch.int32, torch.int64):
+        pid_outer = pid_outer.to(torch.int64)
+    pid = pid_outer.contiguous()
+    outer = my_outer_atoms.contiguous()
+    E = edges.size(1)
+    d = L.HaloDesc()
+    d.n_atoms, d.n_edges, d.num_local, d.my_rank, d.world_size = N, E, outer.size(0), R, W
+    d.pid_dtype = L.DG_I32 if pid.dtype == torch.int32 else L.DG_I64
+    wsb = lib.dg_halo_workspace_size(N, W)
+    _check(wsb > 0, f"extract_halo_info: world_size must be <= 4096, got {W}")
+    with torch.cuda.device(dev):
+        s = L.stream_of(dev)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        send_off = torch.empty(W + 1, dtype=torch.int64, device=dev)
+        recv_off = torch.empty(W + 1, dtype=torch.int64, device=dev)
+        interior = torch.empty(outer.size(0), dtype=torch.bool, device=dev)
+        base = edges.data_ptr()
+        L.check(lib.dg_halo_count(d, L.ctypes.c_void_p(base), L.ctypes.c_void_p(base + 8 * E),
+                                  L.ptr(pid), L.ptr(outer), L.ptr(send_off), L.ptr(recv_off),
+                                  L.ptr(interior), L.ptr(ws), wsb, s), "extract_halo_info")
+        ts, tr = L._i64(0), L._i64(0)
+        L.check(lib.dg_halo_read_totals(L.ptr(ws), ts, tr, s), "extract_halo_info")
+        send_local = torch.empty(ts.value, dtype=torch.int64, device=dev)
+        recv_ghost = torch.empty(tr.value, dtype=torch.int64, device=dev)
+        recv_atom = torch.empty(tr.value, dtype=torch.int64, device=dev)
+        L.check(lib.dg_halo_write(d, L.ptr(pid), L.ptr(send_local), L.ptr(recv_ghost),
+                                  L.ptr(recv_atom), L.ptr(ws), wsb, s), "extract_halo_info")
+    return send_off, send_local, recv_off, recv_ghost, interior, recv_atom
+
+
 def sfc_keys(pos, curve_type=SFCCurveType.Morton):
     """SFC keys of every atom, int64 [N] (sfc_kernels.cu:19-109, bounds :196-198)."""
     _check(isinstance(pos, torch.Tensor) and pos.is_cuda, "pos must be a CUDA tensor")
@@ -316,3 +373,75 @@ def sfc_partition_cuda(pos, weights, W, curve_type):
         L.check(lib.dg_sfc_labels(L.ptr(perm), n, int(W), L.ptr(weights), L.ptr(labels), L.ptr(ws),
                                   wsb, L.stream_of(dev)), "sfc_partition_cuda")
     return labels
+
+
+# ---------------------------------------------------------------------------------------
+# Plain holders of the reference's bound structs that DistGraphBuilder exchanges
+# (dynamis_state_impl.pyi:23-29, 64-85), and the SFC partitioner's partition() for device
+# tensors (partition/sfc_partitioner.cpp:97-195).
+# ---------------------------------------------------------------------------------------
+
+
+class DistEnvironment:
+    """dynamis_state_impl.pyi:23-29."""
+
+    def __init__(self) -> None:
+        self.global_rank = 0
+        self.world_size = 1
+        self.local_rank = 0
+        self.gpus_per_node = 1
+        self.num_nodes = 1
+
+
+class MolecularInfo:
+    """dynamis_state_impl.pyi:64-72 (the fields the partitioner reads)."""
+
+    def __init__(self) -> None:
+        self.num_atoms = 0
+        self.atom_positions = None
+        self.atom_vertex_numbers = None
+        self.edge_counts = None
+        self.atom_types = None
+        self.atom_velocities = None
+        self.atom_forces = None
+
+
+class PartitionMessagePassingInfo:
+    """dynamis_state_impl.pyi:74-85."""
+
+    def __init__(self) -> None:
+        self.partition_id = None
+        self.partition_indices = None
+        self.atom_counts = None
+        self.global_send_recv_matrix = None
+        self.send_offsets = None
+        self.send_local_indices = None
+        self.recv_offsets = None
+        self.recv_ghost_indices = None
+        self.interior_mask = None
+        self.edge_index = None
+        self.edge_index_halo = None
+
+
+class SFCPartitioner:
+    """SFC partitioner (partition/sfc_partitioner.cpp:97-195), device path only."""
+
+    def __init__(self, curve_type=SFCCurveType.Morton) -> None:
+        self.curve_type = SFCCurveType(int(curve_type))
+
+    def partition(self, state: MolecularInfo, env: DistEnvironment) -> PartitionMessagePassingInfo:
+        """Unweighted, or weighted by ``state.edge_counts`` when set (:184-195, :97-179)."""
+        pos = state.atom_positions
+        W, R = int(env.world_size), int(env.global_rank)
+        labels = sfc_partition_cuda(pos.to(torch.float32), state.edge_counts, W, self.curve_type)
+        info = PartitionMessagePassingInfo()
+        info.partition_id = labels
+        mine = torch.nonzero(labels.eq(R), as_tuple=False).squeeze(-1)
+        info.atom_counts = torch.bincount(labels, minlength=W)
+        vn = state.atom_vertex_numbers
+        if vn is None:
+            vn = torch.arange(int(state.num_atoms), dtype=torch.int64, device=pos.device)
+        info.partition_indices = vn.index_select(0, mine)
+        info.global_send_recv_matrix = torch.zeros(W, W, dtype=torch.int64, device=pos.device)
+        info.global_send_recv_matrix[R, R] = mine.numel()
+        return info

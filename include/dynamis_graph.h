@@ -42,7 +42,7 @@ typedef enum {
     DG_ERR_CAPACITY = 5   /* edge capacity smaller than the edge count */
 } dg_status;
 
-typedef enum { DG_F32 = 0, DG_F64 = 1 } dg_dtype;
+typedef enum { DG_F32 = 0, DG_F64 = 1, DG_I64 = 2, DG_I32 = 3 } dg_dtype;
 
 /* Status flag bits of dg_graph_read_totals(). */
 #define DG_FLAG_RANGE 1
@@ -136,6 +136,47 @@ dg_status dg_sfc_order(const int64_t* keys, int64_t n, int64_t* perm, void* work
 dg_status dg_sfc_labels(const int64_t* perm, int64_t n, int64_t n_parts, const int64_t* weights,
                         int64_t* labels, void* workspace, size_t workspace_bytes,
                         hipStream_t stream);
+
+/* Halo send/recv plan of one rank from its edges (every edge's dst in this rank's atom
+ * set).  Replaces extract_halo_info (dist_graph_ops.cpp:38-60,
+ * dist_graph_ops_kernels.cu:104-188; binding dynamis_state_bindings.cpp:256).
+ *   recv: atoms a = src of an edge with pid[a] != my_rank, once each, grouped by peer
+ *         pid[a] ascending, by global id within a peer;
+ *   send: pairs (p, d) with d = dst of an edge whose src is owned by p != my_rank, grouped
+ *         by p, by global id d within a peer; reported as the position of d in my_outer
+ *         (-1 if d is not in my_outer);
+ *   interior_mask[j] = my_outer[j] is the dst of no such edge.
+ * Two stages on one workspace of dg_halo_workspace_size(n_atoms, world_size) bytes:
+ * dg_halo_count (offsets + interior mask), dg_halo_read_totals (synchronous), then
+ * dg_halo_write (the index lists, into buffers of the read sizes). */
+typedef struct dg_halo_desc {
+    int64_t n_atoms;    /* N: length of pid, range of atom ids */
+    int64_t n_edges;    /* E */
+    int64_t num_local;  /* length of my_outer */
+    int64_t my_rank;
+    int64_t world_size; /* 1 .. 4096 */
+    int32_t pid_dtype;  /* DG_I32 or DG_I64 */
+    int32_t pad_;
+} dg_halo_desc;
+
+size_t dg_halo_workspace_size(int64_t n_atoms, int64_t world_size);
+/*   edge_src/edge_dst int64 [n_edges]; pid [n_atoms]; my_outer int64 [num_local]
+ *   send_offsets, recv_offsets  out int64 [world_size+1]
+ *   interior_mask               out uint8 (0/1) [num_local] */
+dg_status dg_halo_count(const dg_halo_desc* desc, const int64_t* edge_src, const int64_t* edge_dst,
+                        const void* pid, const int64_t* my_outer, int64_t* send_offsets,
+                        int64_t* recv_offsets, uint8_t* interior_mask, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
+/* Synchronous.  DG_ERR_RANGE if an edge endpoint, pid value or my_outer entry was out of
+ * range. */
+dg_status dg_halo_read_totals(const void* workspace, int64_t* total_send, int64_t* total_recv,
+                              hipStream_t stream);
+/*   send_local_indices out int64 [total_send]
+ *   recv_ghost_indices out int64 [total_recv]  (num_local + k)
+ *   recv_atom_global   out int64 [total_recv] */
+dg_status dg_halo_write(const dg_halo_desc* desc, const void* pid, int64_t* send_local_indices,
+                        int64_t* recv_ghost_indices, int64_t* recv_atom_global, void* workspace,
+                        size_t workspace_bytes, hipStream_t stream);
 
 /* Message of the last failure on this thread ("" if none). */
 const char* dg_last_error(void);
