@@ -35,6 +35,9 @@ def main():
     ap.add_argument("--config", default="C3")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--path", default="graph", choices=["graph", "halo"],
+                    help="graph: the headline full rebuild; halo: extract_halo_info of one rank "
+                         "of an 8-way SFC partition of the same box (edges at r + 0.5)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -60,6 +63,9 @@ def main():
 
     from dynamis_amd import _lib as L
     from dynamis_amd import configs
+
+    if args.path == "halo":
+        return bench_halo(args)
 
     box = {"C1": configs.fcc, "C2": configs.c2, "C3": configs.c3, "C4": configs.c4,
            "C5": configs.c5}[args.config]()
@@ -212,6 +218,97 @@ def main():
     if pos.dtype == torch.float64:
         out["dtype"] = "fp64 positions, fp64 predicate, int64 edges"
     print(json.dumps(out), flush=True)
+
+
+def bench_halo(args):
+    """extract_halo_info on rank 3 of an 8-way Morton partition of the config's box: the
+    per-rank edges at r + 0.5 are built once; one step = dg_halo_count + dg_halo_write
+    into preallocated outputs."""
+    import numpy as np
+    import torch
+
+    from dynamis_amd import _lib as L
+    from dynamis_amd import configs
+    from dynamis_amd.dynamis_state import dynamis_state_impl as impl
+
+    W, R, skin = 8, 3, 0.5
+    box = {"C2": configs.c2, "C3": configs.c3}[args.config]()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = L.lib()
+    pos = torch.from_numpy(box.pos).to(dev)
+    n = pos.shape[0]
+    pid = impl.sfc_partition_cuda(pos, None, W, 0)
+    my = torch.nonzero(pid.eq(R)).squeeze(-1)
+    ei, _, _, _ = impl.radius_graph_pbc_ex(pos, torch.from_numpy(np.asarray(box.cell)),
+                                           torch.tensor(list(box.pbc)), box.radius + skin, 0, False, my)
+    E = ei.shape[1]
+    d = L.HaloDesc()
+    d.n_atoms, d.n_edges, d.num_local, d.my_rank, d.world_size = n, E, my.numel(), R, W
+    d.pid_dtype = L.DG_I64
+    wsb = lib.dg_halo_workspace_size(n, W)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    so = torch.empty(W + 1, dtype=torch.int64, device=dev)
+    ro = torch.empty(W + 1, dtype=torch.int64, device=dev)
+    im = torch.empty(my.numel(), dtype=torch.bool, device=dev)
+    s = L.stream_of(dev)
+    stream = torch.cuda.current_stream(dev)
+    src_p, dst_p = L.ctypes.c_void_p(ei.data_ptr()), L.ctypes.c_void_p(ei.data_ptr() + 8 * E)
+
+    def count():
+        L.check(lib.dg_halo_count(d, src_p, dst_p, L.ptr(pid), L.ptr(my), L.ptr(so), L.ptr(ro),
+                                  L.ptr(im), L.ptr(ws), wsb, s), "halo count")
+
+    count()
+    ts, tr = L._i64(0), L._i64(0)
+    L.check(lib.dg_halo_read_totals(L.ptr(ws), ts, tr, s), "halo totals")
+    sl = torch.empty(ts.value, dtype=torch.int64, device=dev)
+    rg = torch.empty(tr.value, dtype=torch.int64, device=dev)
+    ra = torch.empty(tr.value, dtype=torch.int64, device=dev)
+
+    def step():
+        count()
+        L.check(lib.dg_halo_write(d, L.ptr(pid), L.ptr(sl), L.ptr(rg), L.ptr(ra), L.ptr(ws), wsb, s),
+                "halo write")
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0 = torch.cuda.Event(enable_timing=True)
+    t1 = torch.cuda.Event(enable_timing=True)
+    t0.record(stream)
+    for _ in range(args.steps):
+        step()
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    # algorithmic bytes: edges (src, dst) + pid[src] per edge; per atom the peer word
+    # (clear, mark, 2 walks, interior), recv flag and global->local entry; the outputs
+    cpu = None
+    if not args.no_cpu:
+        from oracle import halo as ohalo
+
+        e_np, pid_np, my_np = ei.cpu().numpy(), pid.cpu().numpy(), my.cpu().numpy()
+        tc = time.perf_counter()
+        ohalo.extract_halo_info(e_np[0], e_np[1], pid_np, my_np, R, W, n)
+        cs = time.perf_counter() - tc
+        cpu = {"value": round(E / cs / 1e9, 5), "unit": "Gedges/s", "cores": 1, "kind": "port",
+               "sample": f"one extract_halo_info of the same {E} edges by the numpy oracle "
+                         f"(sorted unique, as the reference), {cs * 1e3:.0f} ms"}
+    nbytes = 24 * E + n * (8 * 4 + 3 + 8) + 8 * (ts.value + 2 * tr.value) + 9 * my.numel()
+    ach = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "extract_halo_info edges/s (rank 3 of 8, edges at r+0.5)", "value": round(E / ms / 1e6, 3),
+        "unit": "Gedges/s", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": True, "scaling": "weak", "vs_baseline": None,
+        "dtype": "int64", "data": "synthetic (seeded numpy uniform box)",
+        "config": {"workload": f"halo plan, {args.config} N={n}, W={W}, rank {R}, r={box.radius}+{skin}",
+                   "edges": E, "num_local": int(my.numel()), "total_send": ts.value,
+                   "total_recv": tr.value},
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "dg_halo_count + dg_halo_write (all kernels)", "algorithmic_bytes": nbytes},
+        "cpu_baseline": cpu}), flush=True)
 
 
 if __name__ == "__main__":

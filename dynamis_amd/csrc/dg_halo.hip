@@ -8,7 +8,7 @@
 //   edge pass   one pass over the edges marks recv atoms (a byte per atom) and sets bit p
 //               of a per-atom peer set for every send pair (p, d) (one u64 word per 64
 //               peers; an atomic OR only when the bit is still clear);
-//   count pass  a wave walks 1024 consecutive atom ids and counts, per peer, the atoms of
+//   count pass  a wave walks 256 consecutive atom ids and counts, per peer, the atoms of
 //               each set -- hist[p][unit], peer-major;
 //   scan        one exclusive scan over hist gives every (peer, unit) its output offset:
 //               peer-major order = grouped by peer, ascending id inside a peer, which is
@@ -34,7 +34,7 @@ dg_status fail(dg_status st, const std::string& msg);
 namespace {
 using namespace dg;
 
-constexpr int kUnit = 1024;          // atom ids per wave unit
+constexpr int kUnit = 256;           // atom ids per wave unit
 constexpr int kWaves = 4;            // wave units per workgroup
 constexpr int64_t kMaxWorld = 4096;  // LDS: kWaves * world_size int32 per workgroup
 
@@ -45,7 +45,7 @@ enum : unsigned { kErrEdge = 1, kErrPid = 2, kErrOuter = 4 };
 
 struct Layout {
     int64_t n, W, nw, nu;
-    size_t o_hdr, o_smask, o_rflag, o_g2l, o_hs, o_hr, o_os, o_or, o_part, total;
+    size_t o_hdr, o_smask, o_rflag, o_g2l, o_pid, o_hs, o_hr, o_os, o_or, o_part, total;
 };
 
 Layout layout(int64_t n, int64_t W)
@@ -62,6 +62,7 @@ Layout layout(int64_t n, int64_t W)
     L.o_smask = take(8 * (size_t)n * L.nw);
     L.o_rflag = take((size_t)n);
     L.o_g2l = take(4 * (size_t)n);
+    L.o_pid = take(2 * (size_t)n);
     L.o_hs = take(4 * nh);
     L.o_hr = take(4 * nh);
     L.o_os = take(8 * (nh + 1));
@@ -78,6 +79,8 @@ struct Args {
     unsigned long long* smask;
     uint8_t* rflag;
     int* g2l;
+    uint16_t* pid16;  // pid narrowed to 16 bits (kMaxWorld <= 65535): the edge pass
+                      // gathers it at random, and 2 B/atom stays in L2
 };
 
 __device__ __forceinline__ int64_t pid_at(const void* pid, int dt, int64_t a)
@@ -105,7 +108,7 @@ __device__ __forceinline__ unsigned long long set_word(const Args& A, int64_t a,
 {
     if (RECV) {
         if (!A.rflag[a]) return 0ull;
-        const int64_t p = pid_at(A.pid, A.pid_dt, a);
+        const int64_t p = A.pid16[a];
         return (p >> 6) == w ? 1ull << (p & 63) : 0ull;
     }
     return A.smask[a * A.nw + w];
@@ -119,6 +122,8 @@ __global__ void clear_kernel(Args A, unsigned* hdr)
     if (i < A.n) {
         A.rflag[i] = 0;
         A.g2l[i] = -1;
+        const int64_t p = pid_at(A.pid, A.pid_dt, i);
+        A.pid16[i] = (uint64_t)p < (uint64_t)A.W ? (uint16_t)p : (uint16_t)0xffff;
     }
     if (i < 16) hdr[i] = 0u;
 }
@@ -136,27 +141,55 @@ __global__ void g2l_kernel(Args A, const int64_t* __restrict__ outer, unsigned* 
 }
 
 // dist_graph_ops_kernels.cu:46-58 (boundary_peer_kernel) fused with the recv / send
-// marking that the reference does with unique().
-__global__ void edge_kernel(Args A, const int64_t* __restrict__ src,
-                            const int64_t* __restrict__ dst, int64_t E, unsigned* err)
+// marking that the reference does with unique().  A thread takes kEdgeIlp consecutive
+// edges, so that many pid gathers are in flight.  Edges of one dst arrive together, so a
+// (dst, peer) pair usually repeats on neighbouring edges: only the first edge of a run of
+// equal pairs (compared with the previous edge, across lanes too) touches the peer word.
+constexpr int kEdgeIlp = 4;
+
+__global__ __launch_bounds__(256) void edge_kernel(Args A, const int64_t* __restrict__ src,
+                                                   const int64_t* __restrict__ dst, int64_t E,
+                                                   unsigned* err)
 {
-    const int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    const int64_t s = src[e], d = dst[e];
-    if ((uint64_t)s >= (uint64_t)A.n || (uint64_t)d >= (uint64_t)A.n) {
-        atomicOr(err, (unsigned)kErrEdge);
-        return;
+    const int64_t e0 = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) * kEdgeIlp;
+    int64_t s[kEdgeIlp], d[kEdgeIlp], p[kEdgeIlp];
+    bool ok[kEdgeIlp];
+#pragma unroll
+    for (int k = 0; k < kEdgeIlp; ++k) {
+        const bool in = e0 + k < E;
+        s[k] = in ? src[e0 + k] : 0;
+        d[k] = in ? dst[e0 + k] : -1;
+        ok[k] = in && (uint64_t)s[k] < (uint64_t)A.n && (uint64_t)d[k] < (uint64_t)A.n;
+        if (in && !ok[k]) atomicOr(err, (unsigned)kErrEdge);
     }
-    const int64_t p = pid_at(A.pid, A.pid_dt, s);
-    if ((uint64_t)p >= (uint64_t)A.W) {
-        atomicOr(err, (unsigned)kErrPid);
-        return;
+#pragma unroll
+    for (int k = 0; k < kEdgeIlp; ++k) {
+        p[k] = ok[k] ? (int64_t)A.pid16[s[k]] : A.R;
+        if ((uint64_t)p[k] >= (uint64_t)A.W) {
+            atomicOr(err, (unsigned)kErrPid);
+            ok[k] = false;
+            p[k] = A.R;
+        }
     }
-    if (p == A.R) return;
-    A.rflag[s] = 1;
-    unsigned long long* wp = A.smask + d * A.nw + (p >> 6);
-    const unsigned long long bit = 1ull << (p & 63);
-    if (!(__atomic_load_n(wp, __ATOMIC_RELAXED) & bit)) atomicOr(wp, bit);
+    // pair key of each edge (-1: nothing to mark); the previous lane's last key
+    int64_t key[kEdgeIlp];
+#pragma unroll
+    for (int k = 0; k < kEdgeIlp; ++k) key[k] = (ok[k] && p[k] != A.R) ? d[k] * A.W + p[k] : -1;
+    const unsigned lo = __shfl_up((unsigned)key[kEdgeIlp - 1], 1, 64);
+    const unsigned hi = __shfl_up((unsigned)((uint64_t)key[kEdgeIlp - 1] >> 32), 1, 64);
+    int64_t prev = (threadIdx.x & 63) ? (int64_t)(((uint64_t)hi << 32) | lo) : -1;
+#pragma unroll
+    for (int k = 0; k < kEdgeIlp; ++k) {
+        if (key[k] >= 0) {
+            A.rflag[s[k]] = 1;
+            if (key[k] != prev) {
+                unsigned long long* wp = A.smask + d[k] * A.nw + (p[k] >> 6);
+                const unsigned long long bit = 1ull << (p[k] & 63);
+                if (!(__atomic_load_n(wp, __ATOMIC_RELAXED) & bit)) atomicOr(wp, bit);
+            }
+        }
+        prev = key[k];
+    }
 }
 
 // dist_graph_ops_kernels.cu:178-182: interior = no remote-src edge into the atom.
@@ -272,6 +305,7 @@ Args make_args(const dg_halo_desc* d, const Layout& L, const void* pid, void* ws
     A.smask = (unsigned long long*)(w + L.o_smask);
     A.rflag = (uint8_t*)(w + L.o_rflag);
     A.g2l = (int*)(w + L.o_g2l);
+    A.pid16 = (uint16_t*)(w + L.o_pid);
     return A;
 }
 
@@ -307,7 +341,7 @@ dg_status dg_halo_count(const dg_halo_desc* d, const int64_t* src, const int64_t
     if (d->num_local > 0)
         hipLaunchKernelGGL(g2l_kernel, dim3(nblk(d->num_local)), dim3(256), 0, s, A, my_outer, err);
     if (d->n_edges > 0)
-        hipLaunchKernelGGL(edge_kernel, dim3(nblk(d->n_edges)), dim3(256), 0, s, A, src, dst,
+        hipLaunchKernelGGL(edge_kernel, dim3(nblk((d->n_edges + kEdgeIlp - 1) / kEdgeIlp)), dim3(256), 0, s, A, src, dst,
                            d->n_edges, err);
     if (d->num_local > 0)
         hipLaunchKernelGGL(interior_kernel, dim3(nblk(d->num_local)), dim3(256), 0, s, A, my_outer,
