@@ -298,17 +298,29 @@ __device__ __forceinline__ int64_t xcd_tile_rank(int64_t b, int64_t ntiles)
     return x * q + (x < rem ? x : rem) + j;
 }
 
-struct SearchShared {
+// LDS of one search workgroup.  The count pass keeps only what its sweep reads (so four
+// workgroups fit a CU); the write pass adds the per-entry shift table and the batch's
+// offset / target tables.
+struct SearchSharedBase {
     float4 q[kCap + 1];  // + sentinel
-    uint32_t T[kCap + 1];
     int rp[kMaxRegion + 1];
     int rg[kMaxRegion];
     int tbs[6 * 6 * 6 + 1];  // bin starts of the tile (T <= 6 per axis)
-    int off[kBlock + 1];  // write pass: edge offsets of the batch's targets
-    int tid[kBlock];
-    uint32_t tf[kBlock];
     int64_t w64[kBlock / 64];
     int w32[kBlock / 64];
+};
+template <bool WRITE>
+struct SearchShared;
+template <>
+struct SearchShared<false> : SearchSharedBase {
+    __align__(16) uint16_t lb[kBlock][8];  // per-lane staging of 8 slot entries
+};
+template <>
+struct SearchShared<true> : SearchSharedBase {
+    uint32_t T[kCap + 1];  // packed (bin image shift - source floor) per entry
+    int off[kBlock + 1];   // edge offsets of the batch's targets
+    int tid[kBlock];
+    uint32_t tf[kBlock];
 };
 
 __device__ __forceinline__ void region_offset(const SearchArgs& a, int rx, int ry, int rz,
@@ -377,8 +389,7 @@ template <int MODE>
 __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 {
     constexpr bool WRITE = MODE == 1;
-    __shared__ SearchShared sh;
-    __shared__ __align__(16) uint16_t s_lb[WRITE ? 1 : kBlock][8];
+    __shared__ SearchShared<WRITE> sh;
 
     const int64_t rank = xcd_tile_rank(blockIdx.x, a.ntiles);
     const int lin = a.tile_of_rank[rank];
@@ -456,6 +467,32 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
     const bool one_chunk = nchunks <= 1;
     int loaded = -1;
 
+    // packed (image shift of region bin rb - floor of cell-list entry gidx)
+    auto entry_T = [&](int rb, int gidx) -> uint32_t {
+        const uint32_t fl = a.sflr[gidx];
+        const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+        int sb[3];
+#pragma unroll
+        for (int d = 0; d < 3; ++d) {
+            const int gg = g0[d] - a.P[d] + r[d];
+            sb[d] = a.pbc[d] ? floor_div(gg, a.nb[d]) : 0;
+        }
+        return pack3(sb[0] - unpack3(fl, 0), sb[1] - unpack3(fl, 1), sb[2] - unpack3(fl, 2));
+    };
+    // the same for region entry vreg (count pass: no table; a search over the bin starts)
+    auto cand_T = [&](int vreg) -> uint32_t {
+        if constexpr (WRITE) {
+            return sh.T[vreg % kCap];
+        } else {
+            int lo = 0, hi = a.nregion;
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (sh.rp[mid] <= vreg) lo = mid; else hi = mid;
+            }
+            return entry_T(lo, sh.rg[lo] + (vreg - sh.rp[lo]));
+        }
+    };
+
     auto load_chunk = [&](int c) {
         const int c0 = c * kCap;
         const int c1 = min(total, c0 + kCap);
@@ -469,18 +506,11 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             const int rb = lo;
             const int gidx = sh.rg[rb] + (vv - sh.rp[rb]);
             const float4 e = a.spos[gidx];
-            const uint32_t fl = a.sflr[gidx];
             const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
             float o[3];
             region_offset(a, r[0], r[1], r[2], o);
-            int sb[3];
-#pragma unroll
-            for (int d = 0; d < 3; ++d) {
-                const int gg = g0[d] - a.P[d] + r[d];
-                sb[d] = a.pbc[d] ? floor_div(gg, a.nb[d]) : 0;
-            }
             sh.q[v] = make_float4(e.x + o[0], e.y + o[1], e.z + o[2], e.w);
-            sh.T[v] = pack3(sb[0] - unpack3(fl, 0), sb[1] - unpack3(fl, 1), sb[2] - unpack3(fl, 2));
+            if constexpr (WRITE) sh.T[v] = entry_T(rb, gidx);
         }
     };
     auto ensure_chunk = [&](int c) {  // uniform
@@ -568,7 +598,7 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
                             bool edge = d2 < a.lo_in && d2 > a.tiny;
                             const bool band = !edge && d2 <= a.hi && v != vs;
                             if (__builtin_expect(band, false)) {
-                                const uint32_t Tp = sh.T[v];
+                                const uint32_t Tp = cand_T(c0 + v);
                                 edge = exact_edge(a, __float_as_int(q.w), my_id, unpack3(Tp, 0) + fx,
                                                   unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
                             }
@@ -582,9 +612,9 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             }
         };
 
-        if (!WRITE) {
+        if constexpr (!WRITE) {
             // ---------------- count pass
-            uint16_t* lb = s_lb[threadIdx.x];
+            uint16_t* lb = sh.lb[threadIdx.x];
             const bool slots = one_chunk && a.slot != nullptr;
             uint16_t* myslot = a.slot + (size_t)j * a.K;
             for (int c = 0; c < nchunks; ++c) {
@@ -612,6 +642,7 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             continue;
         }
 
+        if constexpr (WRITE) {
         // ---------------- write pass
         const int mycnt = active ? a.cnt[j] : 0;
         int btot;
@@ -707,6 +738,7 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             }
         }
         ebase += btot;
+        }
         __syncthreads();
     }
 
