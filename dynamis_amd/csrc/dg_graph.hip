@@ -48,6 +48,10 @@ dg_status fail(dg_status st, const std::string& msg)
 constexpr int kCap = 1792;    // region entries staged in LDS per chunk
 constexpr int kRegPerThread = (kMaxRegion + kBlock - 1) / kBlock;
 constexpr int kBinSortMax = 128;
+constexpr int kExpandIlp = 4;  // 64-edge steps per iteration of the expansion
+// search_kernel<1> work of a tile, set by the count pass
+constexpr int kFixOver = 1;     // a target has more than K neighbours
+constexpr int kFixChunked = 2;  // the region does not fit one LDS chunk (or no slots)
 
 // Value known to be uniform across the wave, moved to a scalar register.
 __device__ __forceinline__ int rfl(int x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -260,6 +264,7 @@ struct SearchArgs {
     float hi, lo_in, tiny;
     const float4* spos;
     const uint32_t* sflr;
+    const int* sid;    // atom id of every cell-list entry
     const int* bstart;
     const int* tile_of_rank;
     const int* rank_of_tile;
@@ -274,6 +279,7 @@ struct SearchArgs {
     int* cnt;          // per target, processing order
     int* counts_user;  // per target, caller order (nullable)
     int* ttot;         // per tile (rank order)
+    int* tfix;         // per tile: kFix* bits, work left to search_kernel<1>
     // write pass
     const int64_t* tbase;
     int64_t* out_src;
@@ -299,8 +305,7 @@ __device__ __forceinline__ int64_t xcd_tile_rank(int64_t b, int64_t ntiles)
 }
 
 // LDS of one search workgroup.  The count pass keeps only what its sweep reads (so four
-// workgroups fit a CU); the write pass adds the per-entry shift table and the batch's
-// offset / target tables.
+// workgroups fit a CU); the fix-up write pass adds the per-entry shift table.
 struct SearchSharedBase {
     float4 q[kCap + 1];  // + sentinel
     int rp[kMaxRegion + 1];
@@ -318,9 +323,6 @@ struct SearchShared<false> : SearchSharedBase {
 template <>
 struct SearchShared<true> : SearchSharedBase {
     uint32_t T[kCap + 1];  // packed (bin image shift - source floor) per entry
-    int off[kBlock + 1];   // edge offsets of the batch's targets
-    int tid[kBlock];
-    uint32_t tf[kBlock];
 };
 
 __device__ __forceinline__ void region_offset(const SearchArgs& a, int rx, int ry, int rz,
@@ -381,10 +383,9 @@ __device__ __forceinline__ void emit_edge(const SearchArgs& a, int64_t o, int sr
 // MODE 0 (count): per-target degree, per-tile total, and -- for tiles whose region fits
 //   in one chunk -- the target's neighbours as 2-byte LDS region indices in its slot of
 //   K entries (written 16 bytes at a time through a per-lane LDS buffer).
-// MODE 1 (write): no distance tests: the region is staged again, every output edge of the
-//   tile is mapped to (target, k) and expanded from the slot with full-width coalesced
-//   stores, grouped by target in the SFC order.  Targets with more than K neighbours and
-//   tiles with a chunked region are swept again and written directly.
+// MODE 1 (fix-up write, only tiles the count pass flagged): targets with more than K
+//   neighbours get their edges k >= K by a second sweep, tiles with a chunked region are
+//   swept again and written directly.  Every other edge is written by expand_kernel.
 template <int MODE>
 __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 {
@@ -402,9 +403,13 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
     const int tbeg = tstart[kb], tend = tstart[kb + a.tb];
     const int ntg = tend - tbeg;
     if (ntg == 0) {
-        if (!WRITE && threadIdx.x == 0) a.ttot[rank] = 0;
+        if (!WRITE && threadIdx.x == 0) {
+            a.ttot[rank] = 0;
+            a.tfix[rank] = 0;
+        }
         return;
     }
+    if (WRITE && a.tfix[rank] == 0) return;  // expand_kernel wrote the whole tile
     for (int k = threadIdx.x; k <= a.tb; k += kBlock) sh.tbs[k] = tstart[kb + k];
 
     int64_t ebase = 0;
@@ -524,6 +529,7 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 
     const int nrx = 2 * a.P[0] + 1, nry = 2 * a.P[1] + 1, nrz = 2 * a.P[2] + 1;
     int64_t tile_found = 0;
+    bool over_any = false;
 
     for (int k0 = 0; k0 < ntg; k0 += kBlock) {
         const int nbatch = min(kBlock, ntg - k0);
@@ -637,6 +643,7 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
                 a.cnt[j] = found;
                 if (a.counts_user) a.counts_user[caller] = found;
                 tile_found += found;
+                over_any = over_any || found > a.K;
             }
             __syncthreads();
             continue;
@@ -647,70 +654,11 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
         const int mycnt = active ? a.cnt[j] : 0;
         int btot;
         const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
-        if (active) {
-            sh.off[threadIdx.x] = ex;
-            sh.tid[threadIdx.x] = my_id;
-            sh.tf[threadIdx.x] = my_f;
-        }
-        if (threadIdx.x == 0) sh.off[nbatch] = btot;
-        __syncthreads();  // offsets / target tables visible to the whole workgroup
         if (one_chunk) {
-            ensure_chunk(0);
-            // The batch's edges are split evenly over the waves; each wave walks its range
-            // 64 edges at a time, lane e finding its target by a short forward walk from the
-            // wave's current target (a 64-edge chunk spans one or two targets).  Stores use
-            // 32-bit offsets from the wave's bases and are fully coalesced.
-            {
-                const int lane = threadIdx.x & 63;
-                const int w = threadIdx.x >> 6;
-                const int NWv = kBlock / 64;
-                const bool plain = !a.out_vec && !a.out_dist;
-                const int E0 = (int)(((int64_t)btot * w) / NWv), E1 = (int)(((int64_t)btot * (w + 1)) / NWv);
-                int tcur = 0;
-                {
-                    int lo = 0, hi = nbatch;  // target containing E0
-                    while (hi - lo > 1) {
-                        const int mid = (lo + hi) >> 1;
-                        if (sh.off[mid] <= E0) lo = mid; else hi = mid;
-                    }
-                    tcur = rfl(lo);
-                }
-                const int64_t wbase = ebase + E0;
-                int64_t* __restrict__ ps = a.out_src + wbase;
-                int64_t* __restrict__ pd = a.out_dst + wbase;
-                float* __restrict__ pf = a.out_shift + 3 * wbase;
-                const uint16_t* __restrict__ sl = a.slot + (size_t)(tbeg + k0) * a.K;
-                for (int e0 = E0; e0 < E1; e0 += 64) {
-                    const int e = e0 + lane;
-                    int t = tcur;
-                    if (e < E1) {
-                        while (sh.off[t + 1] <= e) ++t;
-                        const int k = e - sh.off[t];
-                        if (k < a.K) {
-                            const int vk = min((int)sl[(uint32_t)(t * a.K + k)], kCap);
-                            const uint32_t Tp = sh.T[vk];
-                            const uint32_t ft = sh.tf[t];
-                            const int src = __float_as_int(sh.q[vk].w);
-                            const int S0 = unpack3(Tp, 0) + unpack3(ft, 0);
-                            const int S1 = unpack3(Tp, 1) + unpack3(ft, 1);
-                            const int S2 = unpack3(Tp, 2) + unpack3(ft, 2);
-                            const uint32_t r = (uint32_t)(e - E0);
-                            if (plain) {
-                                ps[r] = src;
-                                pd[r] = sh.tid[t];
-                                *(float3*)(pf + 3 * r) = make_float3((float)S0, (float)S1, (float)S2);
-                            } else {
-                                emit_edge(a, wbase + r, src, sh.tid[t], S0, S1, S2);
-                            }
-                        }
-                    }
-                    // next chunk starts in the target of this chunk's last edge
-                    tcur = __builtin_amdgcn_readlane(t, min(63, E1 - e0 - 1));
-                }
-            }
             // targets with more than K neighbours: the rest by a second sweep
             const bool over = active && mycnt > a.K;
             if (__syncthreads_or(over)) {
+                ensure_chunk(0);
                 if (over) {
                     const int64_t base = ebase + ex;
                     sweep(0, [&](int v, int k) {
@@ -745,7 +693,294 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
     if (!WRITE) {
         int64_t tt;
         block_excl_scan<int64_t, kBlock>(tile_found, sh.w64, &tt);
-        if (threadIdx.x == 0) a.ttot[rank] = (int)tt;
+        const bool over = __syncthreads_or(over_any);
+        if (threadIdx.x == 0) {
+            a.ttot[rank] = (int)tt;
+            a.tfix[rank] = (over ? kFixOver : 0) |
+                           ((one_chunk && a.slot != nullptr) ? 0 : kFixChunked);
+        }
+    }
+}
+
+// ---------------------------------------------------------------- edge expansion
+// Cell-list range of the region bins rb = kRegPerThread * threadIdx.x + h of the tile at
+// bin g0 (periodic wrap on pbc axes; empty outside the grid on the others).
+__device__ __forceinline__ int region_bins(const SearchArgs& a, const int* g0, int* rcnt, int* rst)
+{
+    const int R0 = a.R[0], R1 = a.R[1];
+    int sum = 0;
+#pragma unroll
+    for (int h = 0; h < kRegPerThread; ++h) {
+        rcnt[h] = 0;
+        rst[h] = 0;
+        const int rb = kRegPerThread * threadIdx.x + h;
+        if (rb >= a.nregion) continue;
+        const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+        int w[3];
+        bool ok = true;
+#pragma unroll
+        for (int d = 0; d < 3; ++d) {
+            const int gg = g0[d] - a.P[d] + r[d];
+            if (a.pbc[d]) {
+                const int m = gg % a.nb[d];
+                w[d] = m < 0 ? m + a.nb[d] : m;
+            } else {
+                ok = ok && gg >= 0 && gg < a.nb[d];
+                w[d] = gg;
+            }
+        }
+        if (ok) {
+            const int t0 = w[0] / a.T[0], t1 = w[1] / a.T[1], t2 = w[2] / a.T[2];
+            const int l0 = w[0] - t0 * a.T[0], l1 = w[1] - t1 * a.T[1], l2 = w[2] - t2 * a.T[2];
+            const int tl = t0 + a.ntl[0] * (t1 + a.ntl[1] * t2);
+            const int64_t key = (int64_t)a.rank_of_tile[tl] * a.tb + (l0 + a.T[0] * (l1 + a.T[1] * l2));
+            rst[h] = a.bstart[key];
+            rcnt[h] = a.bstart[key + 1] - rst[h];
+        }
+        sum += rcnt[h];
+    }
+    return sum;
+}
+
+typedef float v3f __attribute__((ext_vector_type(3)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+struct ExpandShared {
+    int2 e[kCap + 1];        // per region entry: source atom id, packed (bin shift - floor)
+    int st_src[kBlock / 64][64 * kExpandIlp];  // per-wave staging of aligned edge groups
+    int st_dst[kBlock / 64][64 * kExpandIlp];
+    uint32_t st_S[kBlock / 64][64 * kExpandIlp];
+    int tbs[6 * 6 * 6 + 1];  // bin starts of the tile
+    int off[kBlock + 1];     // edge offsets of the batch's targets
+    int tid[kBlock];
+    uint32_t tf[kBlock];
+    int w32[kBlock / 64];
+};
+
+// Writes every edge held in the count pass's slots: one workgroup per tile (tiles whose
+// region needs several LDS chunks are left to search_kernel<1>).  The region is staged
+// as (source id, shift) pairs only -- 8 bytes per entry -- bin by bin from the cell list.
+// Each batch of up to 256 targets has its edges split evenly over the waves; a wave walks
+// its range 64 edges at a time, lane e finding its target by a short forward walk from
+// the wave's current target, and stores with 32-bit offsets from the wave's bases, fully
+// coalesced.  Edges k >= K of a target are left to search_kernel<1>.
+__global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
+{
+    __shared__ ExpandShared sh;
+    const int64_t rank = xcd_tile_rank(blockIdx.x, a.ntiles);
+    const int* tstart = a.subset ? a.tbstart : a.bstart;
+    const int64_t kb = rank * a.tb;
+    const int tbeg = tstart[kb], tend = tstart[kb + a.tb];
+    const int ntg = tend - tbeg;
+    if (ntg == 0 || (a.tfix[rank] & kFixChunked)) return;
+    int64_t ebase = a.tbase[rank];
+    if (a.tbase[rank + 1] > a.capacity) {
+        if (threadIdx.x == 0)
+            atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
+        return;
+    }
+    const int lin = a.tile_of_rank[rank];
+    const int g0[3] = {(lin % a.ntl[0]) * a.T[0], ((lin / a.ntl[0]) % a.ntl[1]) * a.T[1],
+                       (lin / (a.ntl[0] * a.ntl[1])) * a.T[2]};
+    for (int k = threadIdx.x; k <= a.tb; k += kBlock) sh.tbs[k] = tstart[kb + k];
+
+    // ---- stage the region, bin by bin
+    {
+        int rcnt[kRegPerThread], rst[kRegPerThread];
+        const int mysum = region_bins(a, g0, rcnt, rst);
+        int total;
+        int ex = block_excl_scan<int, kBlock>(mysum, sh.w32, &total);
+        const int R0 = a.R[0], R1 = a.R[1];
+#pragma unroll
+        for (int h = 0; h < kRegPerThread; ++h) {
+            const int rb = kRegPerThread * threadIdx.x + h;
+            if (rcnt[h] > 0) {
+                const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+                int sb[3];
+#pragma unroll
+                for (int d = 0; d < 3; ++d) {
+                    const int gg = g0[d] - a.P[d] + r[d];
+                    sb[d] = a.pbc[d] ? floor_div(gg, a.nb[d]) : 0;
+                }
+                for (int i = 0; i < rcnt[h]; ++i) {
+                    const int gidx = rst[h] + i;
+                    const uint32_t fl = a.sflr[gidx];
+                    sh.e[ex + i] = make_int2(a.sid[gidx], (int)pack3(sb[0] - unpack3(fl, 0),
+                                                                     sb[1] - unpack3(fl, 1),
+                                                                     sb[2] - unpack3(fl, 2)));
+                }
+            }
+            ex += rcnt[h];
+        }
+        if (threadIdx.x == 0) sh.e[kCap] = make_int2(0, 0);
+    }
+
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int NWv = kBlock / 64;
+    const bool plain = !a.out_vec && !a.out_dist;
+    for (int k0 = 0; k0 < ntg; k0 += kBlock) {
+        const int nbatch = min(kBlock, ntg - k0);
+        const int j = tbeg + k0 + threadIdx.x;
+        const bool active = threadIdx.x < nbatch;
+        const int mycnt = active ? a.cnt[j] : 0;
+        int btot;
+        const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
+        if (active) {
+            const int sidx = a.subset ? a.tsidx[j] : j;
+            sh.off[threadIdx.x] = ex;
+            sh.tid[threadIdx.x] = a.sid[sidx];
+            sh.tf[threadIdx.x] = a.sflr[sidx];
+        }
+        if (threadIdx.x == 0) sh.off[nbatch] = btot;
+        __syncthreads();  // region entries and the batch tables visible to all waves
+
+        const int E0 = (int)(((int64_t)btot * w) / NWv), E1 = (int)(((int64_t)btot * (w + 1)) / NWv);
+        int tcur = 0;
+        {
+            int lo = 0, hi = nbatch;  // target containing E0
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (sh.off[mid] <= E0) lo = mid; else hi = mid;
+            }
+            tcur = rfl(lo);
+        }
+        const int64_t wbase = ebase + E0;
+        const uint16_t* __restrict__ sl = a.slot + (size_t)(tbeg + k0) * a.K;
+
+        // Edges [b0, b1) of the batch (b1 - b0 <= 64 * kExpandIlp), lane-strided: edge
+        // b0 + 64u + lane -> source id, target id, packed shift; ok = false past b1 or for
+        // k >= K (left to search_kernel<1>).  All slot loads are issued before the first
+        // entry is looked up.  Advances tcur to the target of edge b1 - 1.
+        auto fetch = [&](int b0, int b1, int* rs, int* rd, uint32_t* rS, bool* rok) {
+            int t = tcur;
+            int tt[kExpandIlp], kk[kExpandIlp];
+#pragma unroll
+            for (int u = 0; u < kExpandIlp; ++u) {
+                const int e = b0 + 64 * u + lane;
+                kk[u] = a.K;
+                tt[u] = t;
+                if (e < b1) {
+                    while (sh.off[t + 1] <= e) ++t;
+                    tt[u] = t;
+                    kk[u] = e - sh.off[t];
+                }
+            }
+            int vk[kExpandIlp];
+#pragma unroll
+            for (int u = 0; u < kExpandIlp; ++u)
+                vk[u] = kk[u] < a.K ? (int)sl[(uint32_t)(tt[u] * a.K + kk[u])] : kCap;
+#pragma unroll
+            for (int u = 0; u < kExpandIlp; ++u) {
+                rok[u] = kk[u] < a.K;
+                const int2 en = sh.e[min(vk[u], kCap)];
+                const uint32_t ft = sh.tf[tt[u]];
+                rs[u] = en.x;
+                rd[u] = sh.tid[tt[u]];
+                rS[u] = pack3(unpack3((uint32_t)en.y, 0) + unpack3(ft, 0),
+                              unpack3((uint32_t)en.y, 1) + unpack3(ft, 1),
+                              unpack3((uint32_t)en.y, 2) + unpack3(ft, 2));
+            }
+            // the lane holding edge b1 - 1 has its target in t
+            tcur = __builtin_amdgcn_readlane(t, (b1 - 1 - b0) & 63);
+        };
+        // per-lane stores of the fetched edges (ranges not aligned to 4 edges, and the
+        // vector / distance outputs)
+        auto store_lanes = [&](int b0, const int* rs, const int* rd, const uint32_t* rS,
+                               const bool* rok) {
+#pragma unroll
+            for (int u = 0; u < kExpandIlp; ++u) {
+                if (!rok[u]) continue;
+                const int64_t o = wbase + (b0 + 64 * u + lane - E0);
+                const int S0 = unpack3(rS[u], 0), S1 = unpack3(rS[u], 1), S2 = unpack3(rS[u], 2);
+                if (plain) {
+                    __builtin_nontemporal_store((int64_t)rs[u], a.out_src + o);
+                    __builtin_nontemporal_store((int64_t)rd[u], a.out_dst + o);
+                    const v3f sv = {(float)S0, (float)S1, (float)S2};
+                    __builtin_nontemporal_store(sv, (v3f*)(a.out_shift + 3 * o));
+                } else {
+                    emit_edge(a, o, rs[u], rd[u], S0, S1, S2);
+                }
+            }
+        };
+
+        int rs[kExpandIlp], rd[kExpandIlp];
+        uint32_t rS[kExpandIlp];
+        bool rok[kExpandIlp];
+        if (!plain) {
+            for (int b0 = E0; b0 < E1; b0 += 64 * kExpandIlp) {
+                fetch(b0, min(E1, b0 + 64 * kExpandIlp), rs, rd, rS, rok);
+                store_lanes(b0, rs, rd, rS, rok);
+            }
+        } else {
+            // Groups of 4 edges that start at a multiple of 4 in the output are staged in
+            // LDS and written as 16-byte stores: 2 for the 4 sources, 2 for the targets, 3
+            // for the shifts, every one 16-byte aligned.  The up-to-3 edges before the first
+            // group and after the last one are stored per lane, so no 16-byte store of this
+            // wave touches another wave's edges.  A slot left to search_kernel<1> (k >= K)
+            // receives a placeholder here and its edge there, later on the same stream.
+            const int head = min((int)((4 - (wbase & 3)) & 3), E1 - E0);
+            const int A0 = E0 + head;
+            const int A1 = A0 + ((E1 - A0) & ~3);
+            if (head > 0) {
+                fetch(E0, A0, rs, rd, rS, rok);
+                store_lanes(E0, rs, rd, rS, rok);
+            }
+            int* st_s = sh.st_src[w];
+            int* st_d = sh.st_dst[w];
+            uint32_t* st_S = sh.st_S[w];
+            for (int b0 = A0; b0 < A1; b0 += 64 * kExpandIlp) {
+                const int b1 = min(A1, b0 + 64 * kExpandIlp);
+                fetch(b0, b1, rs, rd, rS, rok);
+#pragma unroll
+                for (int u = 0; u < kExpandIlp; ++u) {
+                    const int i = 64 * u + lane;
+                    if (b0 + i < b1) { st_s[i] = rs[u]; st_d[i] = rd[u]; st_S[i] = rS[u]; }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int G = (b1 - b0) >> 2;
+                const int64_t gb = wbase + (b0 - E0);  // multiple of 4
+                v4i* __restrict__ os = (v4i*)(a.out_src + gb);
+                v4i* __restrict__ od = (v4i*)(a.out_dst + gb);
+                v4f* __restrict__ of = (v4f*)(a.out_shift + 3 * gb);
+#pragma unroll
+                for (int h = 0; h < 2 * kExpandIlp; h += 2) {
+                    const int c = 32 * h + lane;  // 16-byte chunk: edges 2c, 2c + 1
+                    if (c < 2 * G) {
+                        const v4i vs = {st_s[2 * c], 0, st_s[2 * c + 1], 0};
+                        const v4i vd = {st_d[2 * c], 0, st_d[2 * c + 1], 0};
+                        __builtin_nontemporal_store(vs, os + c);
+                        __builtin_nontemporal_store(vd, od + c);
+                    }
+                }
+#pragma unroll
+                for (int h = 0; h < 3 * kExpandIlp / 4 + 1; ++h) {
+                    const int c = 64 * h + lane;  // 16-byte chunk: shift floats 4c .. 4c + 3
+                    if (c < 3 * G) {
+                        float f[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int fi = 4 * c + i;
+                            f[i] = (float)unpack3(st_S[fi / 3], fi % 3);
+                        }
+                        const v4f vf = {f[0], f[1], f[2], f[3]};
+                        __builtin_nontemporal_store(vf, of + c);
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            if (A1 < E1) {
+                fetch(A1, E1, rs, rd, rS, rok);
+                store_lanes(A1, rs, rd, rS, rok);
+            }
+        }
+        ebase += btot;
+        __syncthreads();  // before the next batch rewrites the tables
     }
 }
 
@@ -948,6 +1183,7 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.hi = p.hi; a.lo_in = p.lo_in; a.tiny = p.tiny;
     a.spos = at<float4>(ws, p.o_spos);
     a.sflr = at<uint32_t>(ws, p.o_sflr);
+    a.sid = at<int>(ws, p.o_sid);
     a.bstart = at<int>(ws, p.o_bstart);
     a.tile_of_rank = at<int>(ws, p.o_tor);
     a.rank_of_tile = at<int>(ws, p.o_rot);
@@ -959,6 +1195,7 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.tslot = at<int>(ws, p.o_tslot);
     a.cnt = at<int>(ws, p.o_cnt);
     a.ttot = at<int>(ws, p.o_ttot);
+    a.tfix = at<int>(ws, p.o_tfix);
     a.tbase = at<int64_t>(ws, p.o_tbase);
     a.totals = at<int64_t>(ws, p.o_tot);
     a.slot = at<uint16_t>(ws, p.o_slot);
@@ -1129,6 +1366,7 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
     a.out_src = edge_src; a.out_dst = edge_dst; a.out_shift = cell_shift;
     a.out_vec = edge_vec; a.out_dist = edge_dist; a.vout_f64 = vec_dtype == DG_F64;
     a.capacity = capacity;
+    hipLaunchKernelGGL(expand_kernel, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
     hipLaunchKernelGGL(search_kernel<1>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
     return check_launch("dg_graph_write");
 }

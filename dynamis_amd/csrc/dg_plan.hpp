@@ -40,7 +40,7 @@ struct Plan {
     size_t o_key, o_rank, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
     size_t o_cflag, o_cpos, o_tor, o_rot;
     size_t o_tkey, o_trank, o_tbcnt, o_tbstart, o_tslot, o_tsidx, o_tcaller;
-    size_t o_cnt, o_ttot, o_tbase, o_part, o_tot, o_slot;
+    size_t o_cnt, o_ttot, o_tfix, o_tbase, o_part, o_tot, o_slot;
     int K = 0;              // neighbour slot entries per target
     size_t ws_bytes = 0;
 };
@@ -192,6 +192,7 @@ inline void plan_layout(Plan& p)
     p.o_cnt = take(4 * nt);
     p.o_slot = take(2 * (size_t)p.K * nt);
     p.o_ttot = take(4 * std::max(ntl, nt));
+    p.o_tfix = take(4 * ntl);
     p.o_tbase = take(8 * (std::max(ntl, nt) + 1));
     // scan partials: one int64 per 2048-item block of the largest scan
     size_t big = std::max(std::max(nbins + 1, nc + 1), std::max(ntl, nt) + 1);
