@@ -3,11 +3,12 @@ of the 1M-atom, r_cut = 6 A uniform box (config C3) on one MI355X.
 
     python bench.py [--gpus 1] [--steps K] [--warmup W] [--config C3] [--no-cpu]
 
-One step = one full rebuild through the C ABI (dg_graph_count + dg_graph_write) into
-preallocated output buffers, positions already resident in HBM, no host sync inside the
-step.  Prints ONE JSON line.  `roofline` is for the dominant kernel (the edge-write search
-pass, search_kernel<1>, the only kernel dg_graph_write launches), timed with HIP events
-on the stream it runs on.  `cpu_baseline` times the CPU oracle (a restatement of the
+One step = one full rebuild through the C ABI (dg_graph_build, issued as its two calls
+dg_graph_count + dg_graph_write) into preallocated output buffers, positions already
+resident in HBM, no host sync inside the step.  Prints ONE JSON line.  `roofline` is for
+the dominant kernel, the edge expansion of the write stage (expand_kernel, followed by the
+search_kernel<1> fix-up pass, which exits at once on tiles without fix-up work), timed
+with HIP events on the stream it runs on.  `cpu_baseline` times the CPU oracle (a restatement of the
 reference algorithm) on the same box on this host.
 """
 from __future__ import annotations
@@ -76,16 +77,12 @@ def main():
     tgt = None if box.targets is None else torch.from_numpy(box.targets).to(dev)
     n = pos.shape[0]
 
-    d = L.GraphDesc()
-    d.n_atoms = n
-    d.has_targets = 0 if tgt is None else 1
-    d.n_targets = 0 if tgt is None else tgt.shape[0]
-    d.pos_dtype = L.DG_F64 if pos.dtype == torch.float64 else L.DG_F32
-    for k, v in enumerate(np.asarray(box.cell, np.float64).reshape(-1)):
-        d.cell[k] = float(v)
-    for k in range(3):
-        d.pbc[k] = 1 if box.pbc[k] else 0
-    d.radius = float(box.radius)
+    from dynamis_amd.dynamis_state import dynamis_state_impl as impl
+
+    # the cell is rounded to the position dtype and the radius to fp32, as the reference
+    # binding does (radius_graph.cpp:7,24)
+    d = impl._desc(pos, torch.from_numpy(np.asarray(box.cell, np.float64)),
+                   torch.tensor([bool(x) for x in box.pbc]), impl._r32(box.radius), tgt)
     nt = n if tgt is None else tgt.shape[0]
 
     wsb = lib.dg_graph_workspace_size(d)
@@ -105,6 +102,8 @@ def main():
     shift = torch.empty((cap, 3), dtype=torch.float32, device=dev)
 
     def step(ev=None):
+        # one full rebuild = dg_graph_build: the count stage (SFC reorder, degrees, tile
+        # offsets) then the write stage, back to back, no host sync
         L.check(lib.dg_graph_count(d, L.ptr(pos), L.ptr(tgt), L.ptr(ws), wsb, L.ptr(counts), s), "count")
         if ev is not None:
             ev[0].record(stream)
@@ -134,7 +133,6 @@ def main():
     ms = total_ms / args.steps
 
     # drop-in Python API (exact-size outputs, one host sync per build)
-    from dynamis_amd.dynamis_state import dynamis_state_impl as impl
 
     cell_t = torch.from_numpy(np.asarray(box.cell))
     pbc_t = torch.tensor(list(box.pbc))
@@ -152,16 +150,16 @@ def main():
     # full-rebuild algorithmic bytes: read positions, keys write+read, sorted cell list
     # write+read, edge outputs
     rebuild_bytes = pos_bytes * n + 16 * n + 40 * n + WRITE_BYTES_PER_EDGE * E
-    # write kernel algorithmic bytes per launch: edge outputs + one read of the sorted cell
-    # list (16 B position/id + 4 B floor) + per-target counts
-    kbytes = WRITE_BYTES_PER_EDGE * E + 20 * n + 4 * nt
+    # write stage, algorithmic bytes per launch: edge outputs + one read of the sorted cell
+    # list (ids and packed floors, 8 B) + per-target counts and slot entries (2 B / edge)
+    kbytes = WRITE_BYTES_PER_EDGE * E + 8 * n + 4 * nt + 2 * E
     achieved = kbytes / (write_ms * 1e-3) / 1e9
 
     # HBM bytes per launch of the write kernel measured by rocprofv3 (FETCH_SIZE +
     # WRITE_SIZE, scaled by a plain copy of known size); recorded in profiles/ by the
     # commands written there, for this config.
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"search_write_{args.config}_traffic.json")
+    tfile = os.path.join(ROOT, "profiles", f"edge_write_{args.config}_traffic.json")
     if os.path.exists(tfile):
         try:
             traffic = json.load(open(tfile)).get("bytes_per_launch")
@@ -175,8 +173,9 @@ def main():
         thr = args.cpu_threads or min(16, os.cpu_count() or 1)
         pos_np = box.pos
         tc = time.perf_counter()
-        o = oracle.radius_graph(pos_np, box.cell, box.pbc, box.radius, target_indices=box.targets,
-                                threads=thr)
+        cell_used = np.asarray(box.cell, np.float64).astype(pos_np.dtype).astype(np.float64)
+        o = oracle.radius_graph(pos_np, cell_used, box.pbc, float(np.float32(box.radius)),
+                                target_indices=box.targets, threads=thr)
         cpu_s = time.perf_counter() - tc
         cpu = {"value": round(len(o["src"]) / cpu_s / 1e9, 5), "unit": "Gedges/s", "cores": thr,
                "kind": "port",
@@ -211,7 +210,7 @@ def main():
         "api_ms_per_rebuild": round(api_ms, 3),
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
-                     "kernel": "search_kernel<1> (edge write)",
+                     "kernel": "expand_kernel (+ search_kernel<1> fix-up): the write stage",
                      "algorithmic_bytes": kbytes},
         "cpu_baseline": cpu,
     }

@@ -48,7 +48,7 @@ dg_status fail(dg_status st, const std::string& msg)
 constexpr int kCap = 1792;    // region entries staged in LDS per chunk
 constexpr int kRegPerThread = (kMaxRegion + kBlock - 1) / kBlock;
 constexpr int kBinSortMax = 128;
-constexpr int kExpandIlp = 4;  // 64-edge steps per iteration of the expansion
+constexpr int kExpandIlp = 2;  // 64-edge steps per iteration of the expansion
 // search_kernel<1> work of a tile, set by the count pass
 constexpr int kFixOver = 1;     // a target has more than K neighbours
 constexpr int kFixChunked = 2;  // the region does not fit one LDS chunk (or no slots)
@@ -281,7 +281,7 @@ struct SearchArgs {
     int* ttot;         // per tile (rank order)
     int* tfix;         // per tile: kFix* bits, work left to search_kernel<1>
     // write pass
-    const int64_t* tbase;
+    int64_t* tbase;
     int64_t* out_src;
     int64_t* out_dst;
     float* out_shift;
@@ -294,9 +294,10 @@ struct SearchArgs {
     int K;
 };
 
-// blockIdx -> tile rank: consecutive workgroups go round-robin to the 8 XCDs, so give
-// each XCD one contiguous range of the Morton order (its own compact region of space,
-// so the halo bins a tile shares with its neighbours hit the same L2).
+// Output order -> tile rank: consecutive workgroups go round-robin to the 8 XCDs, so
+// give each XCD one contiguous range of the Morton order (its own compact region of space, so the halo bins a tile
+// shares with its neighbours hit the same L2).  The output holds the tiles in this
+// order: the 8 Morton ranges interleaved tile by tile.
 __device__ __forceinline__ int64_t xcd_tile_rank(int64_t b, int64_t ntiles)
 {
     const int64_t q = ntiles >> 3, rem = ntiles & 7;
@@ -304,26 +305,54 @@ __device__ __forceinline__ int64_t xcd_tile_rank(int64_t b, int64_t ntiles)
     return x * q + (x < rem ? x : rem) + j;
 }
 
-// LDS of one search workgroup.  The count pass keeps only what its sweep reads (so four
-// workgroups fit a CU); the fix-up write pass adds the per-entry shift table.
-struct SearchSharedBase {
-    float4 q[kCap + 1];  // + sentinel
+// LDS of one search workgroup.
+//   qbuf   the staged region: float4 (position relative to the tile origin, atom id) per
+//          entry while distances are tested; reused as ExpandStage by the expansion;
+//   rt/bt  region bin table (rp: first entry of each region bin, rg: its cell-list start)
+//          while the region is staged; reused as the batch tables of the expansion.
+// The count pass adds the per-lane slot staging (lb) and still fits four workgroups per
+// CU; the fix-up write pass adds the per-entry shift table T.
+constexpr int kStage = 64 * kExpandIlp;  // edges one wave stages per step
+struct ExpandStage {
+    int2 e[kCap + 1];  // per region entry: source atom id, packed (bin shift - floor)
+    int st_src[kBlock / 64][kStage];
+    int st_dst[kBlock / 64][kStage];
+    uint32_t st_S[kBlock / 64][kStage];
+};
+struct RegionTab {
     int rp[kMaxRegion + 1];
     int rg[kMaxRegion];
+};
+struct BatchTab {
+    int off[kBlock + 1];  // edge offsets of the batch's targets
+    int tid[kBlock];
+    uint32_t tf[kBlock];
+};
+constexpr int kQBytes = (int)sizeof(float4) * (kCap + 1);
+static_assert(sizeof(ExpandStage) <= (size_t)kQBytes, "expansion view exceeds the region buffer");
+static_assert(sizeof(BatchTab) <= sizeof(RegionTab), "batch tables exceed the region table");
+
+struct SearchLds {
+    __align__(16) unsigned char qbuf[kQBytes];
+    union {
+        RegionTab rt;
+        BatchTab bt;
+    };
     int tbs[6 * 6 * 6 + 1];  // bin starts of the tile (T <= 6 per axis)
     int64_t w64[kBlock / 64];
     int w32[kBlock / 64];
+    int64_t bc[2];  // workgroup broadcasts
 };
-template <bool WRITE>
-struct SearchShared;
-template <>
-struct SearchShared<false> : SearchSharedBase {
+struct CountLds : SearchLds {
     __align__(16) uint16_t lb[kBlock][8];  // per-lane staging of 8 slot entries
 };
-template <>
-struct SearchShared<true> : SearchSharedBase {
+struct FixLds : SearchLds {
     uint32_t T[kCap + 1];  // packed (bin image shift - source floor) per entry
 };
+template <int MODE>
+struct LdsOf { typedef CountLds type; };
+template <>
+struct LdsOf<1> { typedef FixLds type; };
 
 __device__ __forceinline__ void region_offset(const SearchArgs& a, int rx, int ry, int rz,
                                               float* o)
@@ -373,6 +402,267 @@ __device__ __forceinline__ void emit_edge(const SearchArgs& a, int64_t o, int sr
     }
 }
 
+// ---------------------------------------------------------------- edge expansion
+// Cell-list range of the region bins rb = kRegPerThread * threadIdx.x + h of the tile at
+// bin g0 (periodic wrap on pbc axes; empty outside the grid on the others).
+__device__ __forceinline__ int region_bins(const SearchArgs& a, const int* g0, int* rcnt, int* rst)
+{
+    const int R0 = a.R[0], R1 = a.R[1];
+    int sum = 0;
+#pragma unroll
+    for (int h = 0; h < kRegPerThread; ++h) {
+        rcnt[h] = 0;
+        rst[h] = 0;
+        const int rb = kRegPerThread * threadIdx.x + h;
+        if (rb >= a.nregion) continue;
+        const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+        int w[3];
+        bool ok = true;
+#pragma unroll
+        for (int d = 0; d < 3; ++d) {
+            const int gg = g0[d] - a.P[d] + r[d];
+            if (a.pbc[d]) {
+                const int m = gg % a.nb[d];
+                w[d] = m < 0 ? m + a.nb[d] : m;
+            } else {
+                ok = ok && gg >= 0 && gg < a.nb[d];
+                w[d] = gg;
+            }
+        }
+        if (ok) {
+            const int t0 = w[0] / a.T[0], t1 = w[1] / a.T[1], t2 = w[2] / a.T[2];
+            const int l0 = w[0] - t0 * a.T[0], l1 = w[1] - t1 * a.T[1], l2 = w[2] - t2 * a.T[2];
+            const int tl = t0 + a.ntl[0] * (t1 + a.ntl[1] * t2);
+            const int64_t key = (int64_t)a.rank_of_tile[tl] * a.tb + (l0 + a.T[0] * (l1 + a.T[1] * l2));
+            rst[h] = a.bstart[key];
+            rcnt[h] = a.bstart[key + 1] - rst[h];
+        }
+        sum += rcnt[h];
+    }
+    return sum;
+}
+
+typedef float v3f __attribute__((ext_vector_type(3)));
+typedef float v4f __attribute__((ext_vector_type(4)));
+typedef int v4i __attribute__((ext_vector_type(4)));
+
+// Stages the tile's region into ExpandStage::e as (source atom id, packed bin shift -
+// floor) pairs -- 8 bytes per entry -- bin by bin from the cell list.  The caller has
+// finished every use of the float4 view of the region buffer.
+__device__ __forceinline__ void stage_pairs(const SearchArgs& a, SearchLds& sh, const int* g0)
+{
+    ExpandStage& X = *(ExpandStage*)sh.qbuf;
+    {
+        int rcnt[kRegPerThread], rst[kRegPerThread];
+        const int mysum = region_bins(a, g0, rcnt, rst);
+        int total;
+        int ex = block_excl_scan<int, kBlock>(mysum, sh.w32, &total);
+        const int R0 = a.R[0], R1 = a.R[1];
+#pragma unroll
+        for (int h = 0; h < kRegPerThread; ++h) {
+            const int rb = kRegPerThread * threadIdx.x + h;
+            if (rcnt[h] > 0) {
+                const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+                int sb[3];
+#pragma unroll
+                for (int d = 0; d < 3; ++d) {
+                    const int gg = g0[d] - a.P[d] + r[d];
+                    sb[d] = a.pbc[d] ? floor_div(gg, a.nb[d]) : 0;
+                }
+                for (int i = 0; i < rcnt[h]; ++i) {
+                    const int gidx = rst[h] + i;
+                    const uint32_t fl = a.sflr[gidx];
+                    X.e[ex + i] = make_int2(a.sid[gidx], (int)pack3(sb[0] - unpack3(fl, 0),
+                                                                     sb[1] - unpack3(fl, 1),
+                                                                     sb[2] - unpack3(fl, 2)));
+                }
+            }
+            ex += rcnt[h];
+        }
+        if (threadIdx.x == 0) X.e[kCap] = make_int2(0, 0);
+    }
+
+}
+
+// Writes edge k < K of every target of the tile from its slot (region entries staged by
+// stage_pairs; ebase = output offset of the tile's first edge).  Each batch of up to 256
+// targets has its edges split evenly over the waves; a wave walks its range 64 edges at a
+// time, lane e finding its target by a short forward walk from the wave's current target.
+// Edges k >= K are left to search_kernel<1>.  PLAIN: no vector / distance outputs.
+template <bool PLAIN>
+__device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, int tbeg, int ntg,
+                                            int64_t ebase)
+{
+    ExpandStage& X = *(ExpandStage*)sh.qbuf;
+    BatchTab& B = sh.bt;
+    const int lane = threadIdx.x & 63;
+    const int w = threadIdx.x >> 6;
+    const int NWv = kBlock / 64;
+    constexpr bool plain = PLAIN;
+    for (int k0 = 0; k0 < ntg; k0 += kBlock) {
+        const int nbatch = min(kBlock, ntg - k0);
+        const int j = tbeg + k0 + threadIdx.x;
+        const bool active = threadIdx.x < nbatch;
+        const int mycnt = active ? a.cnt[j] : 0;
+        int btot;
+        const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
+        if (active) {
+            const int sidx = a.subset ? a.tsidx[j] : j;
+            B.off[threadIdx.x] = ex;
+            B.tid[threadIdx.x] = a.sid[sidx];
+            B.tf[threadIdx.x] = a.sflr[sidx];
+        }
+        if (threadIdx.x == 0) B.off[nbatch] = btot;
+        __syncthreads();  // region entries and the batch tables visible to all waves
+
+        const int E0 = (int)(((int64_t)btot * w) / NWv), E1 = (int)(((int64_t)btot * (w + 1)) / NWv);
+        int tcur = 0;
+        {
+            int lo = 0, hi = nbatch;  // target containing E0
+            while (hi - lo > 1) {
+                const int mid = (lo + hi) >> 1;
+                if (B.off[mid] <= E0) lo = mid; else hi = mid;
+            }
+            tcur = rfl(lo);
+        }
+        const int64_t wbase = ebase + E0;
+        const uint16_t* __restrict__ sl = a.slot + (size_t)(tbeg + k0) * a.K;
+
+        // Edges [b0, b1) of the batch (b1 - b0 <= 64 * kExpandIlp), lane-strided: edge
+        // b0 + 64u + lane -> source id, target id, packed shift; ok = false past b1 or for
+        // k >= K (left to search_kernel<1>).  All slot loads are issued before the first
+        // entry is looked up.  Advances tcur to the target of edge b1 - 1.
+        auto fetch = [&](int b0, int b1, int* rs, int* rd, uint32_t* rS, bool* rok) {
+            int t = tcur;
+            int tt[kExpandIlp], kk[kExpandIlp];
+#pragma unroll
+            for (int u = 0; u < kExpandIlp; ++u) {
+                const int e = b0 + 64 * u + lane;
+                kk[u] = a.K;
+                tt[u] = t;
+                if (e < b1) {
+                    while (B.off[t + 1] <= e) ++t;
+                    tt[u] = t;
+                    kk[u] = e - B.off[t];
+                }
+            }
+            int vk[kExpandIlp];
+#pragma unroll
+            for (int u = 0; u < kExpandIlp; ++u)
+                vk[u] = kk[u] < a.K ? (int)sl[(uint32_t)(tt[u] * a.K + kk[u])] : kCap;
+#pragma unroll
+            for (int u = 0; u < kExpandIlp; ++u) {
+                rok[u] = kk[u] < a.K;
+                const int2 en = X.e[min(vk[u], kCap)];
+                const uint32_t ft = B.tf[tt[u]];
+                rs[u] = en.x;
+                rd[u] = B.tid[tt[u]];
+                rS[u] = pack3(unpack3((uint32_t)en.y, 0) + unpack3(ft, 0),
+                              unpack3((uint32_t)en.y, 1) + unpack3(ft, 1),
+                              unpack3((uint32_t)en.y, 2) + unpack3(ft, 2));
+            }
+            // the lane holding edge b1 - 1 has its target in t
+            tcur = __builtin_amdgcn_readlane(t, (b1 - 1 - b0) & 63);
+        };
+        // per-lane stores of the fetched edges (ranges not aligned to 4 edges, and the
+        // vector / distance outputs)
+        auto store_lanes = [&](int b0, const int* rs, const int* rd, const uint32_t* rS,
+                               const bool* rok) {
+#pragma unroll
+            for (int u = 0; u < kExpandIlp; ++u) {
+                if (!rok[u]) continue;
+                const int64_t o = wbase + (b0 + 64 * u + lane - E0);
+                const int S0 = unpack3(rS[u], 0), S1 = unpack3(rS[u], 1), S2 = unpack3(rS[u], 2);
+                if constexpr (plain) {
+                    __builtin_nontemporal_store((int64_t)rs[u], a.out_src + o);
+                    __builtin_nontemporal_store((int64_t)rd[u], a.out_dst + o);
+                    const v3f sv = {(float)S0, (float)S1, (float)S2};
+                    __builtin_nontemporal_store(sv, (v3f*)(a.out_shift + 3 * o));
+                } else {
+                    emit_edge(a, o, rs[u], rd[u], S0, S1, S2);
+                }
+            }
+        };
+
+        int rs[kExpandIlp], rd[kExpandIlp];
+        uint32_t rS[kExpandIlp];
+        bool rok[kExpandIlp];
+        if constexpr (!plain) {
+            for (int b0 = E0; b0 < E1; b0 += 64 * kExpandIlp) {
+                fetch(b0, min(E1, b0 + 64 * kExpandIlp), rs, rd, rS, rok);
+                store_lanes(b0, rs, rd, rS, rok);
+            }
+        } else {
+            // Groups of 4 edges that start at a multiple of 4 in the output are staged in
+            // LDS and written as 16-byte stores: 2 for the 4 sources, 2 for the targets, 3
+            // for the shifts, every one 16-byte aligned.  The up-to-3 edges before the first
+            // group and after the last one are stored per lane, so no 16-byte store of this
+            // wave touches another wave's edges.  A slot left to search_kernel<1> (k >= K)
+            // receives a placeholder here and its edge there, later on the same stream.
+            const int head = min((int)((4 - (wbase & 3)) & 3), E1 - E0);
+            const int A0 = E0 + head;
+            const int A1 = A0 + ((E1 - A0) & ~3);
+            if (head > 0) {
+                fetch(E0, A0, rs, rd, rS, rok);
+                store_lanes(E0, rs, rd, rS, rok);
+            }
+            int* st_s = X.st_src[w];
+            int* st_d = X.st_dst[w];
+            uint32_t* st_S = X.st_S[w];
+            for (int b0 = A0; b0 < A1; b0 += 64 * kExpandIlp) {
+                const int b1 = min(A1, b0 + 64 * kExpandIlp);
+                fetch(b0, b1, rs, rd, rS, rok);
+#pragma unroll
+                for (int u = 0; u < kExpandIlp; ++u) {
+                    const int i = 64 * u + lane;
+                    if (b0 + i < b1) { st_s[i] = rs[u]; st_d[i] = rd[u]; st_S[i] = rS[u]; }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+                const int G = (b1 - b0) >> 2;
+                const int64_t gb = wbase + (b0 - E0);  // multiple of 4
+                v4i* __restrict__ os = (v4i*)(a.out_src + gb);
+                v4i* __restrict__ od = (v4i*)(a.out_dst + gb);
+                v4f* __restrict__ of = (v4f*)(a.out_shift + 3 * gb);
+#pragma unroll
+                for (int h = 0; h < 2 * kExpandIlp; h += 2) {
+                    const int c = 32 * h + lane;  // 16-byte chunk: edges 2c, 2c + 1
+                    if (c < 2 * G) {
+                        const v4i vs = {st_s[2 * c], 0, st_s[2 * c + 1], 0};
+                        const v4i vd = {st_d[2 * c], 0, st_d[2 * c + 1], 0};
+                        __builtin_nontemporal_store(vs, os + c);
+                        __builtin_nontemporal_store(vd, od + c);
+                    }
+                }
+#pragma unroll
+                for (int h = 0; h < 3 * kExpandIlp / 4 + 1; ++h) {
+                    const int c = 64 * h + lane;  // 16-byte chunk: shift floats 4c .. 4c + 3
+                    if (c < 3 * G) {
+                        float f[4];
+#pragma unroll
+                        for (int i = 0; i < 4; ++i) {
+                            const int fi = 4 * c + i;
+                            f[i] = (float)unpack3(st_S[fi / 3], fi % 3);
+                        }
+                        const v4f vf = {f[0], f[1], f[2], f[3]};
+                        __builtin_nontemporal_store(vf, of + c);
+                    }
+                }
+                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+                __builtin_amdgcn_wave_barrier();
+                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            }
+            if (A1 < E1) {
+                fetch(A1, E1, rs, rd, rS, rok);
+                store_lanes(A1, rs, rd, rS, rok);
+            }
+        }
+        ebase += btot;
+        __syncthreads();  // before the next batch rewrites the tables
+    }
+}
+
 // Neighbour search, one tile of bins per workgroup.
 //
 // The region of (T+2P)^3 bins around the tile is staged in LDS (in chunks if it does
@@ -386,13 +676,26 @@ __device__ __forceinline__ void emit_edge(const SearchArgs& a, int64_t o, int sr
 // MODE 1 (fix-up write, only tiles the count pass flagged): targets with more than K
 //   neighbours get their edges k >= K by a second sweep, tiles with a chunked region are
 //   swept again and written directly.  Every other edge is written by expand_kernel.
+// What the count of one tile leaves for the publication / expansion of its edges.
+struct TileOut {
+    int64_t tt;  // edges of the tile
+    int fix;     // kFix* bits
+    int tbeg, ntg;
+    int g0[3];
+};
+
 template <int MODE>
-__global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
+__device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
+                                               typename LdsOf<MODE>::type& sh, int64_t ord)
 {
     constexpr bool WRITE = MODE == 1;
-    __shared__ SearchShared<WRITE> sh;
-
-    const int64_t rank = xcd_tile_rank(blockIdx.x, a.ntiles);
+    float4* const shq = (float4*)sh.qbuf;
+    TileOut out;
+    out.tt = 0;
+    out.fix = 0;
+    // ord: the tile's place in the output (and index of its per-tile records); rank: its
+    // Morton rank.  Tiles go to the output in ord order; ord -> rank is xcd_tile_rank.
+    const int64_t rank = xcd_tile_rank(ord, a.ntiles);
     const int lin = a.tile_of_rank[rank];
     const int tx = lin % a.ntl[0];
     const int ty = (lin / a.ntl[0]) % a.ntl[1];
@@ -402,23 +705,26 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
     const int64_t kb = rank * a.tb;
     const int tbeg = tstart[kb], tend = tstart[kb + a.tb];
     const int ntg = tend - tbeg;
+    out.tbeg = tbeg;
+    out.ntg = ntg;
+    for (int d = 0; d < 3; ++d) out.g0[d] = g0[d];
     if (ntg == 0) {
-        if (!WRITE && threadIdx.x == 0) {
-            a.ttot[rank] = 0;
-            a.tfix[rank] = 0;
+        if (MODE == 0 && threadIdx.x == 0) {
+            a.ttot[ord] = 0;
+            a.tfix[ord] = 0;
         }
-        return;
+        return out;
     }
-    if (WRITE && a.tfix[rank] == 0) return;  // expand_kernel wrote the whole tile
+    if (WRITE && a.tfix[ord] == 0) return out;  // the expansion wrote the whole tile
     for (int k = threadIdx.x; k <= a.tb; k += kBlock) sh.tbs[k] = tstart[kb + k];
 
     int64_t ebase = 0;
     if (WRITE) {
-        ebase = a.tbase[rank];
-        if (a.tbase[rank + 1] > a.capacity) {
+        ebase = a.tbase[ord];
+        if (ebase + a.ttot[ord] > a.capacity) {
             if (threadIdx.x == 0)
                 atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
-            return;
+            return out;
         }
     }
 
@@ -462,10 +768,10 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 #pragma unroll
         for (int h = 0; h < kRegPerThread; ++h) {
             const int rb = kRegPerThread * threadIdx.x + h;
-            if (rb < a.nregion) { sh.rp[rb] = ex; sh.rg[rb] = rst[h]; }
+            if (rb < a.nregion) { sh.rt.rp[rb] = ex; sh.rt.rg[rb] = rst[h]; }
             ex += rcnt[h];
         }
-        if (threadIdx.x == 0) sh.rp[a.nregion] = total;
+        if (threadIdx.x == 0) sh.rt.rp[a.nregion] = total;
     }
     __syncthreads();
     const int nchunks = (total + kCap - 1) / kCap;
@@ -492,9 +798,9 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             int lo = 0, hi = a.nregion;
             while (hi - lo > 1) {
                 const int mid = (lo + hi) >> 1;
-                if (sh.rp[mid] <= vreg) lo = mid; else hi = mid;
+                if (sh.rt.rp[mid] <= vreg) lo = mid; else hi = mid;
             }
-            return entry_T(lo, sh.rg[lo] + (vreg - sh.rp[lo]));
+            return entry_T(lo, sh.rt.rg[lo] + (vreg - sh.rt.rp[lo]));
         }
     };
 
@@ -506,15 +812,15 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             int lo = 0, hi = a.nregion;
             while (hi - lo > 1) {
                 const int mid = (lo + hi) >> 1;
-                if (sh.rp[mid] <= vv) lo = mid; else hi = mid;
+                if (sh.rt.rp[mid] <= vv) lo = mid; else hi = mid;
             }
             const int rb = lo;
-            const int gidx = sh.rg[rb] + (vv - sh.rp[rb]);
+            const int gidx = sh.rt.rg[rb] + (vv - sh.rt.rp[rb]);
             const float4 e = a.spos[gidx];
             const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
             float o[3];
             region_offset(a, r[0], r[1], r[2], o);
-            sh.q[v] = make_float4(e.x + o[0], e.y + o[1], e.z + o[2], e.w);
+            shq[v] = make_float4(e.x + o[0], e.y + o[1], e.z + o[2], e.w);
             if constexpr (WRITE) sh.T[v] = entry_T(rb, gidx);
         }
     };
@@ -561,7 +867,7 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             t0 = e.x + o[0]; t1 = e.y + o[1]; t2 = e.z + o[2];
             // the target's own region entry (same atom, zero shift) is never an edge
             const int rb_self = ((lz + a.P[2]) * R1 + (ly + a.P[1])) * R0 + (lx + a.P[0]);
-            v_self = sh.rp[rb_self] + (sidx - sh.rg[rb_self]);
+            v_self = sh.rt.rp[rb_self] + (sidx - sh.rt.rg[rb_self]);
         }
         const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
 
@@ -591,14 +897,14 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
                         xhi = min((int)floorf((ux + rem) * a.hbinv[0]) + a.P[0], nrx - 1);
                     }
                     const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
-                    const int va = max(sh.rp[rb + xlo], c0) - c0;
-                    const int vb = min(sh.rp[rb + xhi + 1], c1) - c0;
+                    const int va = max(sh.rt.rp[rb + xlo], c0) - c0;
+                    const int vb = min(sh.rt.rp[rb + xhi + 1], c1) - c0;
                     if (va < vb) {
                         // the next candidate's load is issued before this one is tested
-                        float4 qn = sh.q[va];
+                        float4 qn = shq[va];
                         for (int v = va; v < vb; ++v) {
                             const float4 q = qn;
-                            qn = sh.q[min(v + 1, vb - 1)];
+                            qn = shq[min(v + 1, vb - 1)];
                             const float dx = q.x - t0, dyv = q.y - t1, dzv = q.z - t2;
                             const float d2 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
                             bool edge = d2 < a.lo_in && d2 > a.tiny;
@@ -664,7 +970,7 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
                     sweep(0, [&](int v, int k) {
                         if (k >= a.K && k < mycnt) {
                             const uint32_t Tp = sh.T[v];
-                            emit_edge(a, base + k, __float_as_int(sh.q[v].w), my_id,
+                            emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
                                       unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
                         }
                     });
@@ -679,7 +985,7 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
                 sweep(c, [&](int v, int k) {
                     if (k < mycnt) {
                         const uint32_t Tp = sh.T[v];
-                        emit_edge(a, base + k, __float_as_int(sh.q[v].w), my_id,
+                        emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
                                   unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
                     }
                 });
@@ -694,88 +1000,40 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
         int64_t tt;
         block_excl_scan<int64_t, kBlock>(tile_found, sh.w64, &tt);
         const bool over = __syncthreads_or(over_any);
-        if (threadIdx.x == 0) {
-            a.ttot[rank] = (int)tt;
-            a.tfix[rank] = (over ? kFixOver : 0) |
-                           ((one_chunk && a.slot != nullptr) ? 0 : kFixChunked);
+        const int fix = (over ? kFixOver : 0) | ((one_chunk && a.slot != nullptr) ? 0 : kFixChunked);
+        out.tt = tt;
+        out.fix = fix;
+        if (MODE == 0 && threadIdx.x == 0) {
+            a.ttot[ord] = (int)tt;
+            a.tfix[ord] = fix;
         }
     }
+    return out;
 }
 
-// ---------------------------------------------------------------- edge expansion
-// Cell-list range of the region bins rb = kRegPerThread * threadIdx.x + h of the tile at
-// bin g0 (periodic wrap on pbc axes; empty outside the grid on the others).
-__device__ __forceinline__ int region_bins(const SearchArgs& a, const int* g0, int* rcnt, int* rst)
+// MODE 0 (count) and MODE 1 (fix-up write): one tile per workgroup.
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 {
-    const int R0 = a.R[0], R1 = a.R[1];
-    int sum = 0;
-#pragma unroll
-    for (int h = 0; h < kRegPerThread; ++h) {
-        rcnt[h] = 0;
-        rst[h] = 0;
-        const int rb = kRegPerThread * threadIdx.x + h;
-        if (rb >= a.nregion) continue;
-        const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
-        int w[3];
-        bool ok = true;
-#pragma unroll
-        for (int d = 0; d < 3; ++d) {
-            const int gg = g0[d] - a.P[d] + r[d];
-            if (a.pbc[d]) {
-                const int m = gg % a.nb[d];
-                w[d] = m < 0 ? m + a.nb[d] : m;
-            } else {
-                ok = ok && gg >= 0 && gg < a.nb[d];
-                w[d] = gg;
-            }
-        }
-        if (ok) {
-            const int t0 = w[0] / a.T[0], t1 = w[1] / a.T[1], t2 = w[2] / a.T[2];
-            const int l0 = w[0] - t0 * a.T[0], l1 = w[1] - t1 * a.T[1], l2 = w[2] - t2 * a.T[2];
-            const int tl = t0 + a.ntl[0] * (t1 + a.ntl[1] * t2);
-            const int64_t key = (int64_t)a.rank_of_tile[tl] * a.tb + (l0 + a.T[0] * (l1 + a.T[1] * l2));
-            rst[h] = a.bstart[key];
-            rcnt[h] = a.bstart[key + 1] - rst[h];
-        }
-        sum += rcnt[h];
-    }
-    return sum;
+    __shared__ typename LdsOf<MODE>::type sh;
+    search_tile<MODE>(a, sh, blockIdx.x);
 }
 
-typedef float v3f __attribute__((ext_vector_type(3)));
-typedef float v4f __attribute__((ext_vector_type(4)));
-typedef int v4i __attribute__((ext_vector_type(4)));
-
-struct ExpandShared {
-    int2 e[kCap + 1];        // per region entry: source atom id, packed (bin shift - floor)
-    int st_src[kBlock / 64][64 * kExpandIlp];  // per-wave staging of aligned edge groups
-    int st_dst[kBlock / 64][64 * kExpandIlp];
-    uint32_t st_S[kBlock / 64][64 * kExpandIlp];
-    int tbs[6 * 6 * 6 + 1];  // bin starts of the tile
-    int off[kBlock + 1];     // edge offsets of the batch's targets
-    int tid[kBlock];
-    uint32_t tf[kBlock];
-    int w32[kBlock / 64];
-};
-
-// Writes every edge held in the count pass's slots: one workgroup per tile (tiles whose
-// region needs several LDS chunks are left to search_kernel<1>).  The region is staged
-// as (source id, shift) pairs only -- 8 bytes per entry -- bin by bin from the cell list.
-// Each batch of up to 256 targets has its edges split evenly over the waves; a wave walks
-// its range 64 edges at a time, lane e finding its target by a short forward walk from
-// the wave's current target, and stores with 32-bit offsets from the wave's bases, fully
-// coalesced.  Edges k >= K of a target are left to search_kernel<1>.
+// Writes every edge held in the count pass's slots, one workgroup per tile (the write
+// stage of the two-stage build; tiles whose region needs several LDS chunks are left to
+// search_kernel<1>).
 __global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
 {
-    __shared__ ExpandShared sh;
-    const int64_t rank = xcd_tile_rank(blockIdx.x, a.ntiles);
+    __shared__ SearchLds sh;
+    const int64_t ord = blockIdx.x;  // output order, as search_kernel
+    const int64_t rank = xcd_tile_rank(ord, a.ntiles);
     const int* tstart = a.subset ? a.tbstart : a.bstart;
     const int64_t kb = rank * a.tb;
     const int tbeg = tstart[kb], tend = tstart[kb + a.tb];
     const int ntg = tend - tbeg;
-    if (ntg == 0 || (a.tfix[rank] & kFixChunked)) return;
-    int64_t ebase = a.tbase[rank];
-    if (a.tbase[rank + 1] > a.capacity) {
+    if (ntg == 0 || (a.tfix[ord] & kFixChunked)) return;
+    const int64_t ebase = a.tbase[ord];
+    if (ebase + a.ttot[ord] > a.capacity) {
         if (threadIdx.x == 0)
             atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
         return;
@@ -783,205 +1041,11 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
     const int lin = a.tile_of_rank[rank];
     const int g0[3] = {(lin % a.ntl[0]) * a.T[0], ((lin / a.ntl[0]) % a.ntl[1]) * a.T[1],
                        (lin / (a.ntl[0] * a.ntl[1])) * a.T[2]};
-    for (int k = threadIdx.x; k <= a.tb; k += kBlock) sh.tbs[k] = tstart[kb + k];
-
-    // ---- stage the region, bin by bin
-    {
-        int rcnt[kRegPerThread], rst[kRegPerThread];
-        const int mysum = region_bins(a, g0, rcnt, rst);
-        int total;
-        int ex = block_excl_scan<int, kBlock>(mysum, sh.w32, &total);
-        const int R0 = a.R[0], R1 = a.R[1];
-#pragma unroll
-        for (int h = 0; h < kRegPerThread; ++h) {
-            const int rb = kRegPerThread * threadIdx.x + h;
-            if (rcnt[h] > 0) {
-                const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
-                int sb[3];
-#pragma unroll
-                for (int d = 0; d < 3; ++d) {
-                    const int gg = g0[d] - a.P[d] + r[d];
-                    sb[d] = a.pbc[d] ? floor_div(gg, a.nb[d]) : 0;
-                }
-                for (int i = 0; i < rcnt[h]; ++i) {
-                    const int gidx = rst[h] + i;
-                    const uint32_t fl = a.sflr[gidx];
-                    sh.e[ex + i] = make_int2(a.sid[gidx], (int)pack3(sb[0] - unpack3(fl, 0),
-                                                                     sb[1] - unpack3(fl, 1),
-                                                                     sb[2] - unpack3(fl, 2)));
-                }
-            }
-            ex += rcnt[h];
-        }
-        if (threadIdx.x == 0) sh.e[kCap] = make_int2(0, 0);
-    }
-
-    const int lane = threadIdx.x & 63;
-    const int w = threadIdx.x >> 6;
-    const int NWv = kBlock / 64;
-    const bool plain = !a.out_vec && !a.out_dist;
-    for (int k0 = 0; k0 < ntg; k0 += kBlock) {
-        const int nbatch = min(kBlock, ntg - k0);
-        const int j = tbeg + k0 + threadIdx.x;
-        const bool active = threadIdx.x < nbatch;
-        const int mycnt = active ? a.cnt[j] : 0;
-        int btot;
-        const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
-        if (active) {
-            const int sidx = a.subset ? a.tsidx[j] : j;
-            sh.off[threadIdx.x] = ex;
-            sh.tid[threadIdx.x] = a.sid[sidx];
-            sh.tf[threadIdx.x] = a.sflr[sidx];
-        }
-        if (threadIdx.x == 0) sh.off[nbatch] = btot;
-        __syncthreads();  // region entries and the batch tables visible to all waves
-
-        const int E0 = (int)(((int64_t)btot * w) / NWv), E1 = (int)(((int64_t)btot * (w + 1)) / NWv);
-        int tcur = 0;
-        {
-            int lo = 0, hi = nbatch;  // target containing E0
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (sh.off[mid] <= E0) lo = mid; else hi = mid;
-            }
-            tcur = rfl(lo);
-        }
-        const int64_t wbase = ebase + E0;
-        const uint16_t* __restrict__ sl = a.slot + (size_t)(tbeg + k0) * a.K;
-
-        // Edges [b0, b1) of the batch (b1 - b0 <= 64 * kExpandIlp), lane-strided: edge
-        // b0 + 64u + lane -> source id, target id, packed shift; ok = false past b1 or for
-        // k >= K (left to search_kernel<1>).  All slot loads are issued before the first
-        // entry is looked up.  Advances tcur to the target of edge b1 - 1.
-        auto fetch = [&](int b0, int b1, int* rs, int* rd, uint32_t* rS, bool* rok) {
-            int t = tcur;
-            int tt[kExpandIlp], kk[kExpandIlp];
-#pragma unroll
-            for (int u = 0; u < kExpandIlp; ++u) {
-                const int e = b0 + 64 * u + lane;
-                kk[u] = a.K;
-                tt[u] = t;
-                if (e < b1) {
-                    while (sh.off[t + 1] <= e) ++t;
-                    tt[u] = t;
-                    kk[u] = e - sh.off[t];
-                }
-            }
-            int vk[kExpandIlp];
-#pragma unroll
-            for (int u = 0; u < kExpandIlp; ++u)
-                vk[u] = kk[u] < a.K ? (int)sl[(uint32_t)(tt[u] * a.K + kk[u])] : kCap;
-#pragma unroll
-            for (int u = 0; u < kExpandIlp; ++u) {
-                rok[u] = kk[u] < a.K;
-                const int2 en = sh.e[min(vk[u], kCap)];
-                const uint32_t ft = sh.tf[tt[u]];
-                rs[u] = en.x;
-                rd[u] = sh.tid[tt[u]];
-                rS[u] = pack3(unpack3((uint32_t)en.y, 0) + unpack3(ft, 0),
-                              unpack3((uint32_t)en.y, 1) + unpack3(ft, 1),
-                              unpack3((uint32_t)en.y, 2) + unpack3(ft, 2));
-            }
-            // the lane holding edge b1 - 1 has its target in t
-            tcur = __builtin_amdgcn_readlane(t, (b1 - 1 - b0) & 63);
-        };
-        // per-lane stores of the fetched edges (ranges not aligned to 4 edges, and the
-        // vector / distance outputs)
-        auto store_lanes = [&](int b0, const int* rs, const int* rd, const uint32_t* rS,
-                               const bool* rok) {
-#pragma unroll
-            for (int u = 0; u < kExpandIlp; ++u) {
-                if (!rok[u]) continue;
-                const int64_t o = wbase + (b0 + 64 * u + lane - E0);
-                const int S0 = unpack3(rS[u], 0), S1 = unpack3(rS[u], 1), S2 = unpack3(rS[u], 2);
-                if (plain) {
-                    __builtin_nontemporal_store((int64_t)rs[u], a.out_src + o);
-                    __builtin_nontemporal_store((int64_t)rd[u], a.out_dst + o);
-                    const v3f sv = {(float)S0, (float)S1, (float)S2};
-                    __builtin_nontemporal_store(sv, (v3f*)(a.out_shift + 3 * o));
-                } else {
-                    emit_edge(a, o, rs[u], rd[u], S0, S1, S2);
-                }
-            }
-        };
-
-        int rs[kExpandIlp], rd[kExpandIlp];
-        uint32_t rS[kExpandIlp];
-        bool rok[kExpandIlp];
-        if (!plain) {
-            for (int b0 = E0; b0 < E1; b0 += 64 * kExpandIlp) {
-                fetch(b0, min(E1, b0 + 64 * kExpandIlp), rs, rd, rS, rok);
-                store_lanes(b0, rs, rd, rS, rok);
-            }
-        } else {
-            // Groups of 4 edges that start at a multiple of 4 in the output are staged in
-            // LDS and written as 16-byte stores: 2 for the 4 sources, 2 for the targets, 3
-            // for the shifts, every one 16-byte aligned.  The up-to-3 edges before the first
-            // group and after the last one are stored per lane, so no 16-byte store of this
-            // wave touches another wave's edges.  A slot left to search_kernel<1> (k >= K)
-            // receives a placeholder here and its edge there, later on the same stream.
-            const int head = min((int)((4 - (wbase & 3)) & 3), E1 - E0);
-            const int A0 = E0 + head;
-            const int A1 = A0 + ((E1 - A0) & ~3);
-            if (head > 0) {
-                fetch(E0, A0, rs, rd, rS, rok);
-                store_lanes(E0, rs, rd, rS, rok);
-            }
-            int* st_s = sh.st_src[w];
-            int* st_d = sh.st_dst[w];
-            uint32_t* st_S = sh.st_S[w];
-            for (int b0 = A0; b0 < A1; b0 += 64 * kExpandIlp) {
-                const int b1 = min(A1, b0 + 64 * kExpandIlp);
-                fetch(b0, b1, rs, rd, rS, rok);
-#pragma unroll
-                for (int u = 0; u < kExpandIlp; ++u) {
-                    const int i = 64 * u + lane;
-                    if (b0 + i < b1) { st_s[i] = rs[u]; st_d[i] = rd[u]; st_S[i] = rS[u]; }
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                const int G = (b1 - b0) >> 2;
-                const int64_t gb = wbase + (b0 - E0);  // multiple of 4
-                v4i* __restrict__ os = (v4i*)(a.out_src + gb);
-                v4i* __restrict__ od = (v4i*)(a.out_dst + gb);
-                v4f* __restrict__ of = (v4f*)(a.out_shift + 3 * gb);
-#pragma unroll
-                for (int h = 0; h < 2 * kExpandIlp; h += 2) {
-                    const int c = 32 * h + lane;  // 16-byte chunk: edges 2c, 2c + 1
-                    if (c < 2 * G) {
-                        const v4i vs = {st_s[2 * c], 0, st_s[2 * c + 1], 0};
-                        const v4i vd = {st_d[2 * c], 0, st_d[2 * c + 1], 0};
-                        __builtin_nontemporal_store(vs, os + c);
-                        __builtin_nontemporal_store(vd, od + c);
-                    }
-                }
-#pragma unroll
-                for (int h = 0; h < 3 * kExpandIlp / 4 + 1; ++h) {
-                    const int c = 64 * h + lane;  // 16-byte chunk: shift floats 4c .. 4c + 3
-                    if (c < 3 * G) {
-                        float f[4];
-#pragma unroll
-                        for (int i = 0; i < 4; ++i) {
-                            const int fi = 4 * c + i;
-                            f[i] = (float)unpack3(st_S[fi / 3], fi % 3);
-                        }
-                        const v4f vf = {f[0], f[1], f[2], f[3]};
-                        __builtin_nontemporal_store(vf, of + c);
-                    }
-                }
-                __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
-                __builtin_amdgcn_wave_barrier();
-                __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-            }
-            if (A1 < E1) {
-                fetch(A1, E1, rs, rd, rS, rok);
-                store_lanes(A1, rs, rd, rS, rok);
-            }
-        }
-        ebase += btot;
-        __syncthreads();  // before the next batch rewrites the tables
-    }
+    stage_pairs(a, sh, g0);
+    if (!a.out_vec && !a.out_dist)
+        expand_tile<true>(a, sh, tbeg, ntg, ebase);
+    else
+        expand_tile<false>(a, sh, tbeg, ntg, ebase);
 }
 
 // ---------------------------------------------------------------- all-pairs fallback
@@ -1222,6 +1286,52 @@ BruteArgs brute_args(const Plan& p, const void* pos, const int64_t* tgt, void* w
     return b;
 }
 
+// Steps 1-5 of a build: Morton tile ranks, counting sort of the atoms (and of the
+// explicit targets) into the SFC-ordered cell list.
+void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void* ws,
+                 int64_t* totals, hipStream_t s)
+{
+    GridArgs g = grid_args(p);
+    // 1. Morton rank of the tiles
+    int* cflag = at<int>(ws, p.o_cflag);
+    int* cpos = at<int>(ws, p.o_cpos);
+    hipLaunchKernelGGL(tile_flags_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes, cflag);
+    device_excl_scan<int, int>(cflag, p.ncodes, cpos, at<int>(ws, p.o_part), s);
+    hipLaunchKernelGGL(tile_fill_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes,
+                       cflag, cpos, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot));
+    // 2-5. counting sort of the atoms into SFC-ordered bins
+    int* bcnt = at<int>(ws, p.o_bcnt);
+    int* bstart = at<int>(ws, p.o_bstart);
+    hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, bcnt, p.nbins);
+    hipLaunchKernelGGL(bin_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, g, pos, p.f64, p.n,
+                       (const int*)at<int>(ws, p.o_rot), at<uint32_t>(ws, p.o_key),
+                       at<uint32_t>(ws, p.o_rank), bcnt, totals);
+    device_excl_scan<int, int>(bcnt, p.nbins, bstart, at<int>(ws, p.o_part), s);
+    hipLaunchKernelGGL(scatter_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, p.n,
+                       (const uint32_t*)at<uint32_t>(ws, p.o_key),
+                       (const uint32_t*)at<uint32_t>(ws, p.o_rank), (const int*)bstart,
+                       at<int>(ws, p.o_sid));
+    hipLaunchKernelGGL(finish_bins_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, g, pos, p.f64,
+                       p.nbins, (const int*)bstart, at<int>(ws, p.o_sid), at<float4>(ws, p.o_spos),
+                       at<uint32_t>(ws, p.o_sflr), p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr);
+    if (p.subset) {
+        int* tbcnt = at<int>(ws, p.o_tbcnt);
+        int* tbstart = at<int>(ws, p.o_tbstart);
+        hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, tbcnt, p.nbins);
+        hipLaunchKernelGGL(bin_targets_kernel, dim3(nblocks(p.nt)), dim3(256), 0, s, p.nt, p.n,
+                           target_idx, (const uint32_t*)at<uint32_t>(ws, p.o_key),
+                           at<uint32_t>(ws, p.o_tkey), at<uint32_t>(ws, p.o_trank), tbcnt, totals);
+        device_excl_scan<int, int>(tbcnt, p.nbins, tbstart, at<int>(ws, p.o_part), s);
+        hipLaunchKernelGGL(scatter_targets_kernel, dim3(nblocks(p.nt)), dim3(256), 0, s, p.nt,
+                           (const uint32_t*)at<uint32_t>(ws, p.o_tkey),
+                           (const uint32_t*)at<uint32_t>(ws, p.o_trank), (const int*)tbstart,
+                           at<int>(ws, p.o_tslot));
+        hipLaunchKernelGGL(finish_targets_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, p.nbins,
+                           p.n, (const int*)tbstart, at<int>(ws, p.o_tslot), target_idx,
+                           (const int*)at<int>(ws, p.o_inv), at<int>(ws, p.o_tsidx));
+    }
+}
+
 }  // namespace dg
 
 using namespace dg;
@@ -1266,45 +1376,7 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
                            at<int64_t>(ws, p.o_tbase) + p.nt, totals);
         return check_launch("dg_graph_count(brute)");
     }
-    GridArgs g = grid_args(p);
-    // 1. Morton rank of the tiles
-    int* cflag = at<int>(ws, p.o_cflag);
-    int* cpos = at<int>(ws, p.o_cpos);
-    hipLaunchKernelGGL(tile_flags_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes, cflag);
-    device_excl_scan<int, int>(cflag, p.ncodes, cpos, at<int>(ws, p.o_part), s);
-    hipLaunchKernelGGL(tile_fill_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes,
-                       cflag, cpos, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot));
-    // 2-5. counting sort of the atoms into SFC-ordered bins
-    int* bcnt = at<int>(ws, p.o_bcnt);
-    int* bstart = at<int>(ws, p.o_bstart);
-    hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, bcnt, p.nbins);
-    hipLaunchKernelGGL(bin_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, g, pos, p.f64, p.n,
-                       (const int*)at<int>(ws, p.o_rot), at<uint32_t>(ws, p.o_key),
-                       at<uint32_t>(ws, p.o_rank), bcnt, totals);
-    device_excl_scan<int, int>(bcnt, p.nbins, bstart, at<int>(ws, p.o_part), s);
-    hipLaunchKernelGGL(scatter_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, p.n,
-                       (const uint32_t*)at<uint32_t>(ws, p.o_key),
-                       (const uint32_t*)at<uint32_t>(ws, p.o_rank), (const int*)bstart,
-                       at<int>(ws, p.o_sid));
-    hipLaunchKernelGGL(finish_bins_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, g, pos, p.f64,
-                       p.nbins, (const int*)bstart, at<int>(ws, p.o_sid), at<float4>(ws, p.o_spos),
-                       at<uint32_t>(ws, p.o_sflr), p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr);
-    if (p.subset) {
-        int* tbcnt = at<int>(ws, p.o_tbcnt);
-        int* tbstart = at<int>(ws, p.o_tbstart);
-        hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, tbcnt, p.nbins);
-        hipLaunchKernelGGL(bin_targets_kernel, dim3(nblocks(p.nt)), dim3(256), 0, s, p.nt, p.n,
-                           target_idx, (const uint32_t*)at<uint32_t>(ws, p.o_key),
-                           at<uint32_t>(ws, p.o_tkey), at<uint32_t>(ws, p.o_trank), tbcnt, totals);
-        device_excl_scan<int, int>(tbcnt, p.nbins, tbstart, at<int>(ws, p.o_part), s);
-        hipLaunchKernelGGL(scatter_targets_kernel, dim3(nblocks(p.nt)), dim3(256), 0, s, p.nt,
-                           (const uint32_t*)at<uint32_t>(ws, p.o_tkey),
-                           (const uint32_t*)at<uint32_t>(ws, p.o_trank), (const int*)tbstart,
-                           at<int>(ws, p.o_tslot));
-        hipLaunchKernelGGL(finish_targets_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, p.nbins,
-                           p.n, (const int*)tbstart, at<int>(ws, p.o_tslot), target_idx,
-                           (const int*)at<int>(ws, p.o_inv), at<int>(ws, p.o_tsidx));
-    }
+    launch_sort(p, pos, target_idx, ws, totals, s);
     // 6. degrees
     SearchArgs a = search_args(p, pos, ws);
     a.counts_user = counts_out;
@@ -1369,6 +1441,19 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
     hipLaunchKernelGGL(expand_kernel, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
     hipLaunchKernelGGL(search_kernel<1>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
     return check_launch("dg_graph_write");
+}
+
+dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                         void* ws, size_t ws_bytes, int64_t capacity, int32_t* counts_out,
+                         int64_t* edge_src, int64_t* edge_dst, float* cell_shift, void* edge_vec,
+                         void* edge_dist, int32_t vec_dtype, hipStream_t s)
+{
+    // the write pass reads only device-side results of the count pass (per-tile offsets,
+    // slots), so the two run back to back with no host round trip
+    dg_status st = dg_graph_count(desc, pos, target_idx, ws, ws_bytes, counts_out, s);
+    if (st != DG_OK) return st;
+    return dg_graph_write(desc, pos, target_idx, ws, ws_bytes, capacity, edge_src, edge_dst,
+                          cell_shift, edge_vec, edge_dist, vec_dtype, s);
 }
 
 }  // extern "C"

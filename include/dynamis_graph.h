@@ -101,6 +101,20 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
                          int64_t* edge_src, int64_t* edge_dst, float* cell_shift, void* edge_vec,
                          void* edge_dist, int32_t vec_dtype, hipStream_t stream);
 
+/* One-call build into caller-preallocated outputs of `capacity` edges:
+ * dg_graph_count then dg_graph_write, back to back on the stream with no host round trip
+ * (the write pass reads the count pass's per-tile offsets on the device).  Same outputs,
+ * in the same order.  Read the edge count afterwards with dg_graph_read_totals: if it
+ * exceeds `capacity` (DG_ERR_CAPACITY), the tiles that did not fit were skipped -- rebuild
+ * into larger buffers.  This is the caller-owned-buffer form of
+ * radius_graph_pbc_cuda_impl_ex (radius_graph_kernels.cu:480-934), for callers that keep
+ * edge buffers across rebuilds (the molecular-dynamics loop). */
+dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                         void* workspace, size_t workspace_bytes, int64_t capacity,
+                         int32_t* counts_out, int64_t* edge_src, int64_t* edge_dst,
+                         float* cell_shift, void* edge_vec, void* edge_dist, int32_t vec_dtype,
+                         hipStream_t stream);
+
 /* Order-preserving filter of an edge list to radius (keep iff d2 <= radius^2, canonical
  * fp64 d2).  Replaces filter_edges_to_radius (dist_graph_ops.cpp:5-35,
  * dist_graph_ops_kernels.cu:16-43,62-102).

@@ -1,0 +1,114 @@
+"""GPU tests of the one-call build (dg_graph_build, C ABI): it must produce exactly the
+bytes of the two-stage build (dg_graph_count + dg_graph_write, itself checked against
+the oracle in test_gpu_graph.py) -- same edges in the same order, same counts -- on the
+cases that exercise every path of the fused kernel (slot expansion, targets past the slot
+capacity, chunked dense regions, explicit targets, edge vectors), and report the edge
+count with DG_ERR_CAPACITY when the preallocated buffers are too small."""
+import numpy as np
+import pytest
+import torch
+
+import oracle
+from dynamis_amd import _lib as L
+from dynamis_amd import configs
+from dynamis_amd.dynamis_state import dynamis_state_impl as impl
+
+pytestmark = pytest.mark.gpu
+
+
+def _one_call(pos, cell, pbc, r, targets, capacity, vdt=None):
+    lib = L.lib()
+    d = impl._desc(pos, cell, pbc, impl._r32(r), targets)
+    dev = pos.device
+    wsb = lib.dg_graph_workspace_size(d)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    nt = pos.shape[0] if targets is None else targets.shape[0]
+    cnt = torch.empty(nt, dtype=torch.int32, device=dev)
+    ei = torch.full((2, capacity), -7, dtype=torch.int64, device=dev)
+    sh = torch.full((capacity, 3), -7.0, dtype=torch.float32, device=dev)
+    vec = dist = None
+    if vdt is not None:
+        vec = torch.empty((capacity, 3), dtype=vdt, device=dev)
+        dist = torch.empty(capacity, dtype=vdt, device=dev)
+    s = L.stream_of(dev)
+    st = lib.dg_graph_build(d, L.ptr(pos), L.ptr(targets), L.ptr(ws), wsb, capacity, L.ptr(cnt),
+                            L.ctypes.c_void_p(ei.data_ptr()),
+                            L.ctypes.c_void_p(ei.data_ptr() + 8 * capacity), L.ptr(sh), L.ptr(vec),
+                            L.ptr(dist), L.DG_F64 if vdt == torch.float64 else L.DG_F32, s)
+    L.check(st, "dg_graph_build")
+    E, fl = L._i64(0), L._i64(0)
+    st = lib.dg_graph_read_totals(d, L.ptr(ws), E, fl, s)
+    return st, int(E.value), ei, sh, cnt, vec, dist
+
+
+def _cases():
+    out = []
+    b = configs.uniform(60000, seed=31, dtype=np.float32)
+    out.append(("uniform", b.pos, b.cell, b.pbc, b.radius, None))
+    # cases marked "set" hold bins of more than 128 atoms, whose internal order is the
+    # (run-dependent) arrival order: edges are compared as sets there
+    b = configs.c4(scale=0.4)
+    out.append(("c4", b.pos, b.cell, b.pbc, b.radius, None))
+    rng = np.random.default_rng(13)
+    out.append(("dense/set", (rng.uniform(0, 1, (1500, 3)) * 8.0).astype(np.float32), np.eye(3) * 8.0,
+                (True, True, True), 6.0, None))
+    # a clump: targets far past the slot capacity, in a tile whose region fits LDS
+    p = rng.uniform(0, 40.0, (6000, 3))
+    p[:400] = 20.0 + rng.uniform(-1.2, 1.2, (400, 3))
+    out.append(("clump/set", p.astype(np.float32), np.eye(3) * 40.0, (True, True, True), 5.0, None))
+    b = configs.uniform(8000, seed=21, dtype=np.float32)
+    tg = rng.choice(8000, 1500, replace=False)
+    out.append(("targets", b.pos, b.cell, b.pbc, b.radius, np.r_[tg, tg[:40]]))
+    out.append(("partial", b.pos, b.cell, (True, False, True), b.radius, None))
+    return out
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: c[0])
+def test_matches_two_stage_bytes(cuda, case):
+    name, pos, cell, pbc, r, tg = case
+    print(f"\n[case] one-call build {name} N={len(pos)}", flush=True)
+    p = torch.from_numpy(np.ascontiguousarray(pos)).to(cuda)
+    c = torch.from_numpy(np.asarray(cell, np.float64))
+    b = torch.tensor([bool(x) for x in pbc])
+    t = None if tg is None else torch.from_numpy(np.asarray(tg, np.int64)).to(cuda)
+    ei, co, nn, cnt = impl.radius_graph_pbc_ex(p, c, b, r, 0, False, t)
+    E = ei.shape[1]
+    for rep in range(2):  # the second call reuses nothing but must agree again
+        st, E1, ei1, sh1, cnt1, _, _ = _one_call(p, c, b, r, t, E + 5)
+        assert st == L.DG_OK and E1 == E
+        assert torch.equal(cnt1, cnt)
+        if name.endswith("/set"):
+            g = oracle.canonical_sort(ei1[0, :E].cpu().numpy(), ei1[1, :E].cpu().numpy(),
+                                      sh1[:E].cpu().numpy().astype(np.int64))
+            w = oracle.canonical_sort(ei[0].cpu().numpy(), ei[1].cpu().numpy(),
+                                      co.cpu().numpy().astype(np.int64))
+            assert all(np.array_equal(x, y) for x, y in zip(g, w))
+        else:
+            assert torch.equal(ei1[:, :E], ei) and torch.equal(sh1[:E], co)
+        assert bool((ei1[:, E:] == -7).all()) and bool((sh1[E:] == -7.0).all())  # untouched
+
+
+def test_vectors_match(cuda):
+    b = configs.uniform(20000, seed=5, dtype=np.float32)
+    p = torch.from_numpy(b.pos).to(cuda)
+    c = torch.from_numpy(b.cell)
+    bb = torch.tensor([True] * 3)
+    ei, co, nn, cnt, vec, dist = impl.radius_graph_pbc_vectors(p, c, bb, b.radius, None,
+                                                               vector_dtype=torch.float64)
+    E = ei.shape[1]
+    st, E1, ei1, sh1, _, vec1, dist1 = _one_call(p, c, bb, b.radius, None, E, torch.float64)
+    assert st == L.DG_OK and E1 == E
+    assert torch.equal(ei1, ei) and torch.equal(sh1, co)
+    assert torch.equal(vec1, vec) and torch.equal(dist1, dist)
+
+
+def test_capacity_too_small_reports_count(cuda):
+    b = configs.uniform(30000, seed=9, dtype=np.float32)
+    p = torch.from_numpy(b.pos).to(cuda)
+    c = torch.from_numpy(b.cell)
+    bb = torch.tensor([True] * 3)
+    _, _, nn, _ = impl.radius_graph_pbc_ex(p, c, bb, b.radius, 0, False, None)
+    E = int(nn.item())
+    st, E1, ei1, _, _, _, _ = _one_call(p, c, bb, b.radius, None, E // 2)
+    assert st == L.DG_ERR_CAPACITY and E1 == E
+    assert "capacity" in L.lib().dg_last_error().decode()
