@@ -48,7 +48,7 @@ dg_status fail(dg_status st, const std::string& msg)
 constexpr int kCap = 1792;    // region entries staged in LDS per chunk
 constexpr int kRegPerThread = (kMaxRegion + kBlock - 1) / kBlock;
 constexpr int kBinSortMax = 128;
-constexpr int kExpandIlp = 2;  // 64-edge steps per iteration of the expansion
+constexpr int kExpandIlp = 4;  // 64-edge steps per iteration of the expansion
 // search_kernel<1> work of a tile, set by the count pass
 constexpr int kFixOver = 1;     // a target has more than K neighbours
 constexpr int kFixChunked = 2;  // the region does not fit one LDS chunk (or no slots)
