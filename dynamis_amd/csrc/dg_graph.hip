@@ -872,10 +872,11 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
 
         // Sweep this lane's target over the resident chunk c, in the fixed order (dz, dy,
-        // x, atom); on_edge(v, k) receives the chunk-local region index and the running
-        // neighbour number k of every edge.
+        // x, atom); on_cand(v, edge, k) receives every candidate's chunk-local region index,
+        // whether it is an edge, and the running neighbour number k (the edge's number when
+        // it is one).
         int found = 0;
-        auto sweep = [&](int c, auto&& on_edge) {
+        auto sweep = [&](int c, auto&& on_cand) {
             const int c0 = c * kCap;
             const int c1 = min(total, c0 + kCap);
             const int vs = v_self - c0;
@@ -899,26 +900,37 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                     const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
                     const int va = max(sh.rt.rp[rb + xlo], c0) - c0;
                     const int vb = min(sh.rt.rp[rb + xhi + 1], c1) - c0;
-                    if (va < vb) {
-                        // the next candidate's load is issued before this one is tested
-                        float4 qn = shq[va];
-                        for (int v = va; v < vb; ++v) {
-                            const float4 q = qn;
-                            qn = shq[min(v + 1, vb - 1)];
-                            const float dx = q.x - t0, dyv = q.y - t1, dzv = q.z - t2;
-                            const float d2 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
-                            bool edge = d2 < a.lo_in && d2 > a.tiny;
-                            const bool band = !edge && d2 <= a.hi && v != vs;
-                            if (__builtin_expect(band, false)) {
+                    // two candidates per step, both loads issued first (the second may be
+                    // one past the row -- at most the sentinel -- and is then masked); the
+                    // edge test is branch-free, the rare exact test sits behind a
+                    // wave-uniform check, and on_cand sees every candidate in order
+                    for (int v = va; v < vb; v += 2) {
+                        const float4 q0 = shq[v], q1 = shq[v + 1];
+                        const bool in1 = v + 1 < vb;
+                        float dx = q0.x - t0, dyv = q0.y - t1, dzv = q0.z - t2;
+                        const float d20 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
+                        dx = q1.x - t0; dyv = q1.y - t1; dzv = q1.z - t2;
+                        const float d21 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
+                        bool e0 = (d20 < a.lo_in) & (d20 > a.tiny);
+                        bool e1 = in1 & (d21 < a.lo_in) & (d21 > a.tiny);
+                        const bool b0 = !e0 & (d20 <= a.hi) & (v != vs);
+                        const bool b1 = in1 & !e1 & (d21 <= a.hi) & (v + 1 != vs);
+                        if (__builtin_expect(__ballot(b0 | b1) != 0ull, 0)) {
+                            if (b0) {
                                 const uint32_t Tp = cand_T(c0 + v);
-                                edge = exact_edge(a, __float_as_int(q.w), my_id, unpack3(Tp, 0) + fx,
-                                                  unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
+                                e0 = exact_edge(a, __float_as_int(q0.w), my_id, unpack3(Tp, 0) + fx,
+                                                unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
                             }
-                            if (edge) {
-                                on_edge(v, found);
-                                ++found;
+                            if (b1) {
+                                const uint32_t Tp = cand_T(c0 + v + 1);
+                                e1 = exact_edge(a, __float_as_int(q1.w), my_id, unpack3(Tp, 0) + fx,
+                                                unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
                             }
                         }
+                        on_cand(v, e0, found);
+                        found += e0;
+                        on_cand(v + 1, e1, found);
+                        found += e1;
                     }
                 }
             }
@@ -933,14 +945,14 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 ensure_chunk(c);
                 if (!active) continue;
                 if (slots) {
-                    sweep(c, [&](int v, int k) {
-                        if (k < a.K) {
-                            lb[k & 7] = (uint16_t)v;
-                            if ((k & 7) == 7) *(uint4*)(myslot + (k - 7)) = *(const uint4*)lb;
-                        }
+                    sweep(c, [&](int v, bool e, int k) {
+                        // the entry of slot k is written for every candidate (an edge
+                        // keeps it: k advances); 8 entries go out when an edge fills them
+                        lb[k & 7] = (uint16_t)v;
+                        if (e && (k & 7) == 7 && k < a.K) *(uint4*)(myslot + (k - 7)) = *(const uint4*)lb;
                     });
                 } else {
-                    sweep(c, [&](int, int) {});
+                    sweep(c, [&](int, bool, int) {});
                 }
             }
             if (active) {
@@ -967,8 +979,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 ensure_chunk(0);
                 if (over) {
                     const int64_t base = ebase + ex;
-                    sweep(0, [&](int v, int k) {
-                        if (k >= a.K && k < mycnt) {
+                    sweep(0, [&](int v, bool e, int k) {
+                        if (e && k >= a.K && k < mycnt) {
                             const uint32_t Tp = sh.T[v];
                             emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
                                       unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
@@ -982,8 +994,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             for (int c = 0; c < nchunks; ++c) {
                 ensure_chunk(c);
                 if (!active) continue;
-                sweep(c, [&](int v, int k) {
-                    if (k < mycnt) {
+                sweep(c, [&](int v, bool e, int k) {
+                    if (e && k < mycnt) {
                         const uint32_t Tp = sh.T[v];
                         emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
                                   unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
