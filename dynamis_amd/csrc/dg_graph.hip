@@ -136,10 +136,13 @@ __device__ __forceinline__ uint32_t bin_key(const GridArgs& g, const int* b,
     return (uint32_t)rank_of_tile[lin] * (uint32_t)g.tb + (uint32_t)(l0 + g.T[0] * (l1 + g.T[1] * l2));
 }
 
+// Per atom: wrap, bin, SFC key and an atomic slot inside the key's bin; and the atom's
+// cell-list record (fp32 position relative to its bin origin, packed floor), which
+// finish_bins moves to the atom's sorted place.
 __global__ void bin_atoms_kernel(GridArgs g, const void* __restrict__ pos, int f64, int64_t n,
                                  const int* __restrict__ rank_of_tile, uint32_t* __restrict__ key,
                                  uint32_t* __restrict__ rank, int* __restrict__ bcnt,
-                                 int64_t* __restrict__ totals)
+                                 float4* __restrict__ rec, int64_t* __restrict__ totals)
 {
     int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (i >= n) return;
@@ -151,6 +154,16 @@ __global__ void bin_atoms_kernel(GridArgs g, const void* __restrict__ pos, int f
     uint32_t k = bin_key(g, b, rank_of_tile);
     key[i] = k;
     rank[i] = (uint32_t)atomicAdd(&bcnt[k], 1);
+    // position relative to the bin origin: (s - b/nb) . C
+    double o[3];
+#pragma unroll
+    for (int d = 0; d < 3; ++d) o[d] = s[d] - (double)b[d] / (double)g.nb[d];
+    float4 e;
+    e.x = (float)fma(o[2], g.C[6], fma(o[1], g.C[3], o[0] * g.C[0]));
+    e.y = (float)fma(o[2], g.C[7], fma(o[1], g.C[4], o[0] * g.C[1]));
+    e.z = (float)fma(o[2], g.C[8], fma(o[1], g.C[5], o[0] * g.C[2]));
+    e.w = __uint_as_float(pack3(f[0], f[1], f[2]));
+    rec[i] = e;
 }
 
 __global__ void scatter_atoms_kernel(int64_t n, const uint32_t* __restrict__ key,
@@ -179,32 +192,20 @@ __device__ __forceinline__ void small_sort(int* a, int lo, int hi)
 // One thread per bin: stable (by atom id) order inside the bin, then the SoA cell list.
 // Bins with more than kBinSortMax atoms keep the atomic arrival order (edge set and
 // counts are unaffected; only the order of edges within a target can then vary).
-__global__ void finish_bins_kernel(GridArgs g, const void* __restrict__ pos, int f64,
-                                   int64_t nbins, const int* __restrict__ bstart,
-                                   int* __restrict__ sid, float4* __restrict__ spos,
-                                   uint32_t* __restrict__ sflr, int* __restrict__ inv)
+__global__ void finish_bins_kernel(int64_t nbins, const int* __restrict__ bstart,
+                                   int* __restrict__ sid, const float4* __restrict__ rec,
+                                   float4* __restrict__ spos, uint32_t* __restrict__ sflr,
+                                   int* __restrict__ inv)
 {
     int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (q >= nbins) return;
     int lo = bstart[q], hi = bstart[q + 1];
     if (hi - lo > 1 && hi - lo <= kBinSortMax) small_sort(sid, lo, hi);
     for (int j = lo; j < hi; ++j) {
-        int i = sid[j];
-        double p[3], s[3];
-        int f[3], b[3];
-        load_pos(pos, f64, i, p);
-        wrap_atom(g, p, f, s, b);
-        // position relative to the bin origin: (s - b/nb) . C
-        double o[3];
-#pragma unroll
-        for (int d = 0; d < 3; ++d) o[d] = s[d] - (double)b[d] / (double)g.nb[d];
-        float4 e;
-        e.x = (float)fma(o[2], g.C[6], fma(o[1], g.C[3], o[0] * g.C[0]));
-        e.y = (float)fma(o[2], g.C[7], fma(o[1], g.C[4], o[0] * g.C[1]));
-        e.z = (float)fma(o[2], g.C[8], fma(o[1], g.C[5], o[0] * g.C[2]));
-        e.w = __int_as_float(i);
-        spos[j] = e;
-        sflr[j] = pack3(f[0], f[1], f[2]);
+        const int i = sid[j];
+        const float4 r = rec[i];
+        spos[j] = make_float4(r.x, r.y, r.z, __int_as_float(i));
+        sflr[j] = __float_as_uint(r.w);
         if (inv) inv[i] = j;
     }
 }
@@ -1171,11 +1172,6 @@ __global__ void zero_i64_kernel(int64_t* __restrict__ p, int64_t n)
     if (i < n) p[i] = 0;
 }
 
-__global__ void copy_total_kernel(const int64_t* __restrict__ src, int64_t* __restrict__ totals)
-{
-    if (threadIdx.x == 0 && blockIdx.x == 0) totals[0] = src[0];
-}
-
 inline unsigned nblocks(int64_t n, int b = 256) { return (unsigned)((n + b - 1) / b); }
 
 template <typename T>
@@ -1308,7 +1304,7 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
     int* cflag = at<int>(ws, p.o_cflag);
     int* cpos = at<int>(ws, p.o_cpos);
     hipLaunchKernelGGL(tile_flags_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes, cflag);
-    device_excl_scan<int, int>(cflag, p.ncodes, cpos, at<int>(ws, p.o_part), s);
+    excl_scan<int, int>(cflag, p.ncodes, cpos, at<int>(ws, p.o_part), s);
     hipLaunchKernelGGL(tile_fill_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes,
                        cflag, cpos, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot));
     // 2-5. counting sort of the atoms into SFC-ordered bins
@@ -1317,15 +1313,16 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
     hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, bcnt, p.nbins);
     hipLaunchKernelGGL(bin_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, g, pos, p.f64, p.n,
                        (const int*)at<int>(ws, p.o_rot), at<uint32_t>(ws, p.o_key),
-                       at<uint32_t>(ws, p.o_rank), bcnt, totals);
+                       at<uint32_t>(ws, p.o_rank), bcnt, at<float4>(ws, p.o_rec), totals);
     device_excl_scan<int, int>(bcnt, p.nbins, bstart, at<int>(ws, p.o_part), s);
     hipLaunchKernelGGL(scatter_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, p.n,
                        (const uint32_t*)at<uint32_t>(ws, p.o_key),
                        (const uint32_t*)at<uint32_t>(ws, p.o_rank), (const int*)bstart,
                        at<int>(ws, p.o_sid));
-    hipLaunchKernelGGL(finish_bins_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, g, pos, p.f64,
-                       p.nbins, (const int*)bstart, at<int>(ws, p.o_sid), at<float4>(ws, p.o_spos),
-                       at<uint32_t>(ws, p.o_sflr), p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr);
+    hipLaunchKernelGGL(finish_bins_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, p.nbins,
+                       (const int*)bstart, at<int>(ws, p.o_sid), (const float4*)at<float4>(ws, p.o_rec),
+                       at<float4>(ws, p.o_spos), at<uint32_t>(ws, p.o_sflr),
+                       p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr);
     if (p.subset) {
         int* tbcnt = at<int>(ws, p.o_tbcnt);
         int* tbstart = at<int>(ws, p.o_tbstart);
@@ -1382,10 +1379,8 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
         BruteArgs b = brute_args(p, pos, target_idx, ws);
         b.counts_user = counts_out;
         hipLaunchKernelGGL(brute_kernel<false>, dim3(nblocks(p.nt, 64)), dim3(64), 0, s, b);
-        device_excl_scan<int, int64_t>(at<int>(ws, p.o_cnt), p.nt, at<int64_t>(ws, p.o_tbase),
-                                       at<int64_t>(ws, p.o_part), s);
-        hipLaunchKernelGGL(copy_total_kernel, dim3(1), dim3(64), 0, s,
-                           at<int64_t>(ws, p.o_tbase) + p.nt, totals);
+        excl_scan<int, int64_t>(at<int>(ws, p.o_cnt), p.nt, at<int64_t>(ws, p.o_tbase),
+                                at<int64_t>(ws, p.o_part), s, totals);
         return check_launch("dg_graph_count(brute)");
     }
     launch_sort(p, pos, target_idx, ws, totals, s);
@@ -1393,11 +1388,9 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
     SearchArgs a = search_args(p, pos, ws);
     a.counts_user = counts_out;
     hipLaunchKernelGGL(search_kernel<0>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
-    // 7. tile offsets in SFC order
-    device_excl_scan<int, int64_t>(at<int>(ws, p.o_ttot), p.ntiles, at<int64_t>(ws, p.o_tbase),
-                                   at<int64_t>(ws, p.o_part), s);
-    hipLaunchKernelGGL(copy_total_kernel, dim3(1), dim3(64), 0, s,
-                       at<int64_t>(ws, p.o_tbase) + p.ntiles, totals);
+    // 7. tile offsets in output order, and the total
+    excl_scan<int, int64_t>(at<int>(ws, p.o_ttot), p.ntiles, at<int64_t>(ws, p.o_tbase),
+                            at<int64_t>(ws, p.o_part), s, totals);
     return check_launch("dg_graph_count");
 }
 

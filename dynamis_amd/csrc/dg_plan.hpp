@@ -37,7 +37,7 @@ struct Plan {
     int kimg[3];            // brute path: |S_d| range on periodic axes
     float hi = 0, lo_in = 0, tiny = 0;
     // workspace layout (byte offsets)
-    size_t o_key, o_rank, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
+    size_t o_key, o_rank, o_rec, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
     size_t o_cflag, o_cpos, o_tor, o_rot;
     size_t o_tkey, o_trank, o_tbcnt, o_tbstart, o_tslot, o_tsidx, o_tcaller;
     size_t o_cnt, o_ttot, o_tfix, o_tbase, o_part, o_tot, o_slot;
@@ -172,6 +172,7 @@ inline void plan_layout(Plan& p)
     p.o_tot = take(8 * 8);
     p.o_key = take(4 * n);
     p.o_rank = take(4 * n);
+    p.o_rec = take(16 * n);
     p.o_bcnt = take(4 * nbins);
     p.o_bstart = take(4 * (nbins + 1));
     p.o_sid = take(4 * n);

@@ -115,4 +115,61 @@ inline void device_excl_scan(const Tin* in, int64_t n, Tout* out, Tout* part, hi
                        s, in, n, part, out);
 }
 
+// Exclusive scan of in[0..n) into out[0..n] (out[n] = sum) by one workgroup, for short
+// arrays (one launch instead of three); the sum is also stored to *sum_out if given.
+template <typename Tin, typename Tout>
+__global__ __launch_bounds__(kScanBlock) void small_scan_kernel(const Tin* __restrict__ in,
+                                                                int64_t n, Tout* __restrict__ out,
+                                                                int64_t* __restrict__ sum_out)
+{
+    __shared__ Tout s_w[kScanBlock / 64];
+    Tout carry = 0;
+    for (int64_t b0 = 0; b0 < n; b0 += kScanTile) {
+        const int64_t base = b0 + (int64_t)threadIdx.x * kScanItems;
+        Tout v[kScanItems], sum = 0;
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            v[k] = base + k < n ? (Tout)in[base + k] : (Tout)0;
+            sum += v[k];
+        }
+        Tout tot;
+        Tout ex = block_excl_scan<Tout, kScanBlock>(sum, s_w, &tot) + carry;
+#pragma unroll
+        for (int k = 0; k < kScanItems; ++k) {
+            if (base + k < n) out[base + k] = ex;
+            ex += v[k];
+        }
+        carry += tot;
+    }
+    if (threadIdx.x == 0) {
+        out[n] = carry;
+        if (sum_out) *sum_out = (int64_t)carry;
+    }
+}
+
+template <typename Tout>
+__global__ void copy_sum_kernel(const Tout* __restrict__ src, int64_t* __restrict__ dst)
+{
+    if (threadIdx.x == 0 && blockIdx.x == 0) *dst = (int64_t)*src;
+}
+
+constexpr int64_t kSmallScanMax = 8192;  // one workgroup takes ~2.4 us per 2048 items
+
+// Exclusive scan choosing the one-workgroup kernel for short arrays (it beats three
+// launches up to a few thousand items).
+template <typename Tin, typename Tout>
+inline void excl_scan(const Tin* in, int64_t n, Tout* out, Tout* part, hipStream_t s,
+                      int64_t* sum_out = nullptr)
+{
+    if (n <= kSmallScanMax) {
+        hipLaunchKernelGGL((small_scan_kernel<Tin, Tout>), dim3(1), dim3(kScanBlock), 0, s, in, n,
+                           out, sum_out);
+        return;
+    }
+    device_excl_scan<Tin, Tout>(in, n, out, part, s);
+    if (sum_out)
+        hipLaunchKernelGGL((copy_sum_kernel<Tout>), dim3(1), dim3(64), 0, s, (const Tout*)(out + n),
+                           sum_out);
+}
+
 }  // namespace dg
