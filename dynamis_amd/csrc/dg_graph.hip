@@ -533,37 +533,53 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, 
         // b0 + 64u + lane -> source id, target id, packed shift; ok = false past b1 or for
         // k >= K (left to search_kernel<1>).  All slot loads are issued before the first
         // entry is looked up.  Advances tcur to the target of edge b1 - 1.
-        auto fetch = [&](int b0, int b1, int* rs, int* rd, uint32_t* rS, bool* rok) {
+        // Two halves: locate() finds (target, k) of edges [b0, b1) and issues their slot
+        // loads -- unconditionally (edges past b1 or with k >= K load a valid dummy), so all
+        // kExpandIlp loads are in flight together -- and advances tcur to the target of
+        // edge b1 - 1; resolve() turns them into (source id, target id, packed shift).  The
+        // plain path locates the next step before storing this one, so the wait on its
+        // loads does not also wait on the stores (the memory counter is shared).
+        struct Loc {
+            int tt[kExpandIlp], kk[kExpandIlp], raw[kExpandIlp];
+        };
+        auto locate = [&](int b0, int b1, Loc& L) {
             int t = tcur;
-            int tt[kExpandIlp], kk[kExpandIlp];
 #pragma unroll
             for (int u = 0; u < kExpandIlp; ++u) {
                 const int e = b0 + 64 * u + lane;
-                kk[u] = a.K;
-                tt[u] = t;
+                L.kk[u] = a.K;
+                L.tt[u] = t;
                 if (e < b1) {
                     while (B.off[t + 1] <= e) ++t;
-                    tt[u] = t;
-                    kk[u] = e - B.off[t];
+                    L.tt[u] = t;
+                    L.kk[u] = e - B.off[t];
                 }
             }
-            int vk[kExpandIlp];
-#pragma unroll
-            for (int u = 0; u < kExpandIlp; ++u)
-                vk[u] = kk[u] < a.K ? (int)sl[(uint32_t)(tt[u] * a.K + kk[u])] : kCap;
 #pragma unroll
             for (int u = 0; u < kExpandIlp; ++u) {
-                rok[u] = kk[u] < a.K;
-                const int2 en = X.e[min(vk[u], kCap)];
-                const uint32_t ft = B.tf[tt[u]];
+                const uint32_t at = L.kk[u] < a.K ? (uint32_t)(L.tt[u] * a.K + L.kk[u]) : 0u;
+                L.raw[u] = (int)sl[at];
+            }
+            // the lane holding edge b1 - 1 has its target in t
+            tcur = __builtin_amdgcn_readlane(t, (b1 - 1 - b0) & 63);
+        };
+        auto resolve = [&](const Loc& L, int* rs, int* rd, uint32_t* rS, bool* rok) {
+#pragma unroll
+            for (int u = 0; u < kExpandIlp; ++u) {
+                rok[u] = L.kk[u] < a.K;
+                const int2 en = X.e[rok[u] ? min(L.raw[u], kCap) : kCap];
+                const uint32_t ft = B.tf[L.tt[u]];
                 rs[u] = en.x;
-                rd[u] = B.tid[tt[u]];
+                rd[u] = B.tid[L.tt[u]];
                 rS[u] = pack3(unpack3((uint32_t)en.y, 0) + unpack3(ft, 0),
                               unpack3((uint32_t)en.y, 1) + unpack3(ft, 1),
                               unpack3((uint32_t)en.y, 2) + unpack3(ft, 2));
             }
-            // the lane holding edge b1 - 1 has its target in t
-            tcur = __builtin_amdgcn_readlane(t, (b1 - 1 - b0) & 63);
+        };
+        auto fetch = [&](int b0, int b1, int* rs, int* rd, uint32_t* rS, bool* rok) {
+            Loc L;
+            locate(b0, b1, L);
+            resolve(L, rs, rd, rS, rok);
         };
         // per-lane stores of the fetched edges (ranges not aligned to 4 edges, and the
         // vector / distance outputs)
@@ -610,14 +626,17 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, 
             int* st_s = X.st_src[w];
             int* st_d = X.st_dst[w];
             uint32_t* st_S = X.st_S[w];
+            Loc L;
+            if (A0 < A1) locate(A0, min(A1, A0 + 64 * kExpandIlp), L);
             for (int b0 = A0; b0 < A1; b0 += 64 * kExpandIlp) {
                 const int b1 = min(A1, b0 + 64 * kExpandIlp);
-                fetch(b0, b1, rs, rd, rS, rok);
+                resolve(L, rs, rd, rS, rok);
 #pragma unroll
                 for (int u = 0; u < kExpandIlp; ++u) {
                     const int i = 64 * u + lane;
                     if (b0 + i < b1) { st_s[i] = rs[u]; st_d[i] = rd[u]; st_S[i] = rS[u]; }
                 }
+                if (b1 < A1) locate(b1, min(A1, b1 + 64 * kExpandIlp), L);  // next step's loads
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
