@@ -48,7 +48,7 @@ dg_status fail(dg_status st, const std::string& msg)
 constexpr int kCap = 1792;    // region entries staged in LDS per chunk
 constexpr int kRegPerThread = (kMaxRegion + kBlock - 1) / kBlock;
 constexpr int kBinSortMax = 128;
-constexpr int kExpandIlp = 4;  // 64-edge steps per iteration of the expansion
+constexpr int kExpandIlp = 4;  // 64-edge steps per iteration of the expansion (even)
 // search_kernel<1> work of a tile, set by the count pass
 constexpr int kFixOver = 1;     // a target has more than K neighbours
 constexpr int kFixChunked = 2;  // the region does not fit one LDS chunk (or no slots)
@@ -561,7 +561,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, 
                 L.raw[u] = (int)sl[at];
             }
             // the lane holding edge b1 - 1 has its target in t
-            tcur = __builtin_amdgcn_readlane(t, (b1 - 1 - b0) & 63);
+            if (b1 > b0) tcur = __builtin_amdgcn_readlane(t, (b1 - 1 - b0) & 63);
         };
         auto resolve = [&](const Loc& L, int* rs, int* rd, uint32_t* rS, bool* rok) {
 #pragma unroll
@@ -626,29 +626,33 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, 
             int* st_s = X.st_src[w];
             int* st_d = X.st_dst[w];
             uint32_t* st_S = X.st_S[w];
-            Loc L;
-            if (A0 < A1) locate(A0, min(A1, A0 + 64 * kExpandIlp), L);
-            for (int b0 = A0; b0 < A1; b0 += 64 * kExpandIlp) {
-                const int b1 = min(A1, b0 + 64 * kExpandIlp);
-                resolve(L, rs, rd, rS, rok);
+            // Full steps of 64 * kExpandIlp edges run branch-free: the next step's slot loads
+            // are issued before this step's stores and consumed right behind them, in
+            // straight-line code, so the wait on the loads leaves the stores in flight (the
+            // memory counter is shared by loads and stores).  The last, partial step is
+            // masked.
+            constexpr int kStep = 64 * kExpandIlp;
+            const int nfull = (A1 - A0) / kStep;
+            auto stage = [&](int n) {
 #pragma unroll
                 for (int u = 0; u < kExpandIlp; ++u) {
                     const int i = 64 * u + lane;
-                    if (b0 + i < b1) { st_s[i] = rs[u]; st_d[i] = rd[u]; st_S[i] = rS[u]; }
+                    if (i < n) { st_s[i] = rs[u]; st_d[i] = rd[u]; st_S[i] = rS[u]; }
                 }
-                if (b1 < A1) locate(b1, min(A1, b1 + 64 * kExpandIlp), L);  // next step's loads
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
-                const int G = (b1 - b0) >> 2;
-                const int64_t gb = wbase + (b0 - E0);  // multiple of 4
+            };
+            // 16-byte stores of n staged edges (n a multiple of 4) starting at output gb
+            auto store_groups = [&](int64_t gb, int n, auto full) {
+                const int G = n >> 2;
                 v4i* __restrict__ os = (v4i*)(a.out_src + gb);
                 v4i* __restrict__ od = (v4i*)(a.out_dst + gb);
                 v4f* __restrict__ of = (v4f*)(a.out_shift + 3 * gb);
 #pragma unroll
-                for (int h = 0; h < 2 * kExpandIlp; h += 2) {
-                    const int c = 32 * h + lane;  // 16-byte chunk: edges 2c, 2c + 1
-                    if (c < 2 * G) {
+                for (int h = 0; h < kExpandIlp / 2; ++h) {
+                    const int c = 64 * h + lane;  // 16-byte chunk: edges 2c, 2c + 1
+                    if (full || c < 2 * G) {
                         const v4i vs = {st_s[2 * c], 0, st_s[2 * c + 1], 0};
                         const v4i vd = {st_d[2 * c], 0, st_d[2 * c + 1], 0};
                         __builtin_nontemporal_store(vs, os + c);
@@ -656,9 +660,9 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, 
                     }
                 }
 #pragma unroll
-                for (int h = 0; h < 3 * kExpandIlp / 4 + 1; ++h) {
+                for (int h = 0; h < 3 * kExpandIlp / 4; ++h) {
                     const int c = 64 * h + lane;  // 16-byte chunk: shift floats 4c .. 4c + 3
-                    if (c < 3 * G) {
+                    if (full || c < 3 * G) {
                         float f[4];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
@@ -672,6 +676,20 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, 
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+            };
+            if (A0 < A1) fetch(A0, min(A1, A0 + kStep), rs, rd, rS, rok);
+            for (int s0 = 0; s0 < nfull; ++s0) {
+                const int b0 = A0 + s0 * kStep;
+                stage(kStep);
+                Loc L;
+                locate(b0 + kStep, min(A1, b0 + 2 * kStep), L);  // empty past A1: dummy loads
+                store_groups(wbase + (b0 - E0), kStep, std::true_type());
+                resolve(L, rs, rd, rS, rok);
+            }
+            if (nfull * kStep < A1 - A0) {
+                const int b0 = A0 + nfull * kStep;
+                stage(A1 - b0);
+                store_groups(wbase + (b0 - E0), A1 - b0, std::false_type());
             }
             if (A1 < E1) {
                 fetch(A1, E1, rs, rd, rS, rok);
