@@ -45,7 +45,6 @@ dg_status fail(dg_status st, const std::string& msg)
     return st;
 }
 
-constexpr int kCap = 1792;    // region entries staged in LDS per chunk
 constexpr int kRegPerThread = (kMaxRegion + kBlock - 1) / kBlock;
 constexpr int kBinSortMax = 128;
 constexpr int kExpandIlp = 4;  // 64-edge steps per iteration of the expansion (even)
@@ -339,7 +338,7 @@ struct SearchLds {
         RegionTab rt;
         BatchTab bt;
     };
-    int tbs[6 * 6 * 6 + 1];  // bin starts of the tile (T <= 6 per axis)
+    int tbs[kTileMax * kTileMax * kTileMax + 1];  // bin starts of the tile
     int64_t w64[kBlock / 64];
     int w32[kBlock / 64];
     int64_t bc[2];  // workgroup broadcasts

@@ -20,6 +20,8 @@ namespace dg {
 constexpr int kBlock = 256;      // threads per search workgroup (4 x wave64)
 constexpr int kMaxRegion = 768;  // region bins staged per tile
 constexpr int kTileTargets = 235; // aim: targets per tile <= this (a 256-lane workgroup)
+constexpr int kTileMax = 6;       // bins per tile along one axis
+constexpr int kCap = 1792;        // region entries staged in LDS per chunk
 
 struct Plan {
     int64_t n = 0, nt = 0;  // atoms, targets
@@ -98,16 +100,21 @@ inline void plan_grid(Plan& p)
     // Tile: as many bins as keep the expected targets of a tile within one 256-lane
     // workgroup, with a region of at most kMaxRegion bins; prefer compact tiles.
     {
-        const double per_bin = (double)std::max<int64_t>(p.subset ? p.nt : p.n, 1) /
-                               ((double)p.nb[0] * p.nb[1] * p.nb[2]);
+        const double bins = (double)p.nb[0] * p.nb[1] * p.nb[2];
+        const double per_bin = (double)std::max<int64_t>(p.subset ? p.nt : p.n, 1) / bins;
+        const double src_per_bin = (double)std::max<int64_t>(p.n, 1) / bins;
         int best[3] = {1, 1, 1};
         double best_score = -1;
-        for (int a = 1; a <= std::min(6, p.nb[0]); ++a)
-            for (int b = 1; b <= std::min(6, p.nb[1]); ++b)
-                for (int c = 1; c <= std::min(6, p.nb[2]); ++c) {
+        for (int a = 1; a <= std::min(kTileMax, p.nb[0]); ++a)
+            for (int b = 1; b <= std::min(kTileMax, p.nb[1]); ++b)
+                for (int c = 1; c <= std::min(kTileMax, p.nb[2]); ++c) {
                     const int64_t reg = (int64_t)(a + 2 * p.P[0]) * (b + 2 * p.P[1]) * (c + 2 * p.P[2]);
                     if (reg > kMaxRegion) continue;
                     if (a * b * c * per_bin > kTileTargets && a * b * c > 1) continue;
+                    // the region's atoms fit one LDS chunk with 4 standard deviations to spare
+                    // (a chunked tile is written by the slow direct path)
+                    const double ra = (double)reg * src_per_bin;
+                    if (ra + 4.0 * sqrt(ra) > kCap && a * b * c > 1) continue;
                     // most bins per tile first, then the least halo per bin
                     const double score = a * b * c * 1e6 - (double)reg / (a * b * c);
                     if (score > best_score) { best_score = score; best[0] = a; best[1] = b; best[2] = c; }
