@@ -256,8 +256,10 @@ struct SearchArgs {
     double C[9];
     double hC[9];  // bin step vectors: row d = C[d] / nb[d]
     double r2;
-    int ortho;     // orthorhombic cell with positive diagonal: stencil rows are trimmed
-    float hb[3], hbinv[3], rprune2, pmargin;
+    int lowtri;    // lower-triangular cell (a along x, b in the xy plane, positive diagonal):
+                   // stencil rows are trimmed to the padded cutoff sphere
+    float hax, hbx, hby, hcx, hcy, hcz;  // bin step vectors C[d] / nb[d] (lower triangle)
+    float rprune2, pmargin;
     int nb[3], P[3], T[3], ntl[3], R[3], pbc[3];
     int tb, nregion;
     int64_t ntiles;
@@ -704,7 +706,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, 
 //
 // The region of (T+2P)^3 bins around the tile is staged in LDS (in chunks if it does
 // not fit).  Both passes share the per-target sweep below (one lane per target, rows of
-// the stencil trimmed to the cutoff sphere for orthorhombic cells), so they agree on
+// the stencil trimmed to the cutoff sphere for lower-triangular cells), so they agree on
 // every edge and on its order.
 //
 // MODE 0 (count): per-target degree, per-tile total, and -- for tiles whose region fits
@@ -907,6 +909,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             v_self = sh.rt.rp[rb_self] + (sidx - sh.rt.rg[rb_self]);
         }
         const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
+        // the target's position inside its bin in bin units (lower-triangular cells)
+        const float Oz = uz / a.hcz, Oy = (uy - Oz * a.hcy) / a.hby, Ox = (ux - Oy * a.hbx - Oz * a.hcx) / a.hax;
 
         // Sweep this lane's target over the resident chunk c, in the fixed order (dz, dy,
         // x, atom); on_cand(v, edge, k) receives every candidate's chunk-local region index,
@@ -920,19 +924,26 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             for (int oz = 0; oz < nrz; ++oz) {
                 for (int oy = 0; oy < nry; ++oy) {
                     int xlo = 0, xhi = nrx - 1;
-                    if (a.ortho) {
-                        // gaps from the target to the row's slab along y and z; keep only the
-                        // bins along x that the (padded) cutoff sphere reaches
-                        const int py = oy - a.P[1], pz = oz - a.P[2];
-                        float gy = py > 0 ? py * a.hb[1] - uy : (py < 0 ? uy + (-py - 1) * a.hb[1] : 0.f);
-                        float gz = pz > 0 ? pz * a.hb[2] - uz : (pz < 0 ? uz + (-pz - 1) * a.hb[2] : 0.f);
+                    if (a.lowtri) {
+                        // bounding box of the row (bins py, pz relative to the target's bin,
+                        // all x) in Cartesian y and z, from the target: its gaps gy, gz bound
+                        // the distance from below; the x range that the (padded) cutoff sphere
+                        // can reach then follows from the row's x shear
+                        const float py = (float)(oy - a.P[1]) - Oy, pz = (float)(oz - a.P[2]) - Oz;
+                        const float zl = pz * a.hcz, zh = zl + a.hcz;
+                        const float cyl = fminf(pz * a.hcy, (pz + 1.f) * a.hcy);
+                        const float cyh = fmaxf(pz * a.hcy, (pz + 1.f) * a.hcy);
+                        const float yl = py * a.hby + cyl, yh = (py + 1.f) * a.hby + cyh;
+                        float gy = fmaxf(fmaxf(yl, -yh), 0.f), gz = fmaxf(fmaxf(zl, -zh), 0.f);
                         gy = fmaxf(gy - a.pmargin, 0.f);
                         gz = fmaxf(gz - a.pmargin, 0.f);
                         const float rem2 = a.rprune2 - gy * gy - gz * gz;
                         if (rem2 < 0.f) continue;
                         const float rem = sqrtf(rem2);
-                        xlo = max((int)floorf((ux - rem) * a.hbinv[0]) + a.P[0], 0);
-                        xhi = min((int)floorf((ux + rem) * a.hbinv[0]) + a.P[0], nrx - 1);
+                        const float sl = fminf(py * a.hbx, (py + 1.f) * a.hbx) + fminf(pz * a.hcx, (pz + 1.f) * a.hcx);
+                        const float sh = fmaxf(py * a.hbx, (py + 1.f) * a.hbx) + fmaxf(pz * a.hcx, (pz + 1.f) * a.hcx);
+                        xlo = max((int)floorf(Ox + (-rem - sh) / a.hax) + a.P[0], 0);
+                        xhi = min((int)floorf(Ox + (rem - sl) / a.hax) + a.P[0], nrx - 1);
                     }
                     const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
                     const int va = max(sh.rt.rp[rb + xlo], c0) - c0;
@@ -1271,12 +1282,14 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     for (int d = 0; d < 3; ++d)
         for (int c = 0; c < 3; ++c) a.hC[3 * d + c] = p.C[3 * d + c] / (double)p.nb[d];
     a.r2 = p.r2;
-    a.ortho = p.C[1] == 0.0 && p.C[2] == 0.0 && p.C[3] == 0.0 && p.C[5] == 0.0 && p.C[6] == 0.0 &&
-              p.C[7] == 0.0 && p.C[0] > 0.0 && p.C[4] > 0.0 && p.C[8] > 0.0;
-    for (int d = 0; d < 3; ++d) {
-        a.hb[d] = (float)(p.C[4 * d] / p.nb[d]);
-        a.hbinv[d] = (float)(p.nb[d] / p.C[4 * d]);
-    }
+    a.lowtri = p.C[1] == 0.0 && p.C[2] == 0.0 && p.C[5] == 0.0 && p.C[0] > 0.0 && p.C[4] > 0.0 &&
+               p.C[8] > 0.0;
+    a.hax = (float)(p.C[0] / p.nb[0]);
+    a.hbx = (float)(p.C[3] / p.nb[1]);
+    a.hby = (float)(p.C[4] / p.nb[1]);
+    a.hcx = (float)(p.C[6] / p.nb[2]);
+    a.hcy = (float)(p.C[7] / p.nb[2]);
+    a.hcz = (float)(p.C[8] / p.nb[2]);
     // row trimming must never drop a candidate the exact test could accept: pad the
     // cutoff by far more than the fp32 position error
     a.pmargin = (float)(1e-4 * p.r + 1e-3);
