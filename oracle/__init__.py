@@ -19,9 +19,11 @@ Pinning (what checks each function; see tests/test_oracle.py):
   * ``filter_edges``        -- filter(build(r+skin), r) == build(r) as sets.
   * ``morton_keys``         -- spread identities, decode(encode) round trip with an
                                independent decoder, magic-number form in the HIP build.
-  * ``hilbert_keys``        -- parity unpinned beyond properties (range, b=0 pass-through
-                               bits, determinism): the only other statements of this
-                               custom transform are the reference's own two restatements.
+  * ``hilbert_keys``        -- exhaustive over all 128^3 quantised cells against
+                               oracle/sfc_twin.py, a second restatement that follows the
+                               reference's CPU twin (sfc_partitioner.cpp:50-92) instead of
+                               the CUDA kernel this file follows; range, b=0 pass-through.
+  * ``morton_keys`` (again) -- against the CPU twin's bit loop (sfc_partitioner.cpp:21-45).
   * ``sfc_labels``          -- closed-form balance (unweighted), exact integer cut rule
                                (weighted) on hand-checked cases.
 """

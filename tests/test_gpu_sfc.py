@@ -57,3 +57,15 @@ def test_partition_labels(cuda, curve, W):
     w = np.random.default_rng(1).integers(0, 200, 50_000)
     labw = impl.sfc_partition_cuda(pt, torch.from_numpy(w).to(cuda), W, curve).cpu().numpy()
     assert np.array_equal(labw, oracle.sfc_labels(perm, W, w))
+
+
+def test_hilbert_keys_exhaustive_grid(cuda):
+    """All 128^3 quantised cells (plus the two bounding corners): GPU "Hilbert" keys equal
+    the restatement of the reference's CPU twin (sfc_partitioner.cpp:50-92) cell by cell."""
+    from oracle import sfc_twin
+
+    print("\n[case] hilbert keys, exhaustive 128^3 grid", flush=True)
+    pos, X, Y, Z = sfc_twin.grid_positions(128, 1.0)
+    k = impl.sfc_keys(torch.from_numpy(pos).to(cuda), 1).cpu().numpy()
+    assert np.array_equal(k[:-2], sfc_twin.hilbert_from_grid(X, Y, Z))
+    assert np.array_equal(k, oracle.hilbert_keys(pos))

@@ -174,3 +174,31 @@ def test_sfc_labels_closed_form():
     lw = oracle.sfc_labels(perm, W, w)
     cs = np.cumsum(w[perm])
     assert np.array_equal(lw[perm], np.minimum(cs * W // cs[-1], W - 1))
+
+
+def test_hilbert_exhaustive_vs_cpu_twin():
+    """Every one of the 128^3 quantised cells: the oracle (restating the CUDA kernel,
+    sfc_kernels.cu:62-109) equals the restatement of the reference's CPU twin
+    (sfc_partitioner.cpp:50-92)."""
+    from oracle import sfc_twin
+
+    pos, X, Y, Z = sfc_twin.grid_positions(128, 1.0)
+    k = oracle.hilbert_keys(pos)[:-2]
+    assert np.array_equal(k, sfc_twin.hilbert_from_grid(X, Y, Z))
+    assert len(np.unique(k)) < len(k)  # the transform is not injective; equality is the pin
+
+
+def test_morton_grid_vs_cpu_twin():
+    from oracle import sfc_twin
+
+    # Morton quantises by 2^21 - 1: a 2^21-1 wide box makes cell centres land on integers
+    rng = np.random.default_rng(2)
+    cells = rng.integers(0, 2 ** 21 - 1, (20000, 3))
+    pos = np.concatenate([(cells + 0.5), np.zeros((1, 3)), np.full((1, 3), 2 ** 21 - 1.0)])
+    # fp32 cannot hold 2^21 + 0.5 exactly; quantise in double on the CPU-twin side instead
+    p32 = pos.astype(np.float32)
+    mn, rg = oracle.sfc_bounds(p32)
+    q = np.clip(((p32.astype(np.float32) - mn) / rg * np.float32(2 ** 21 - 1)).astype(np.float32)
+                .astype(np.int64), 0, 2 ** 21 - 1)
+    k = oracle.morton_keys(p32)
+    assert np.array_equal(k, sfc_twin.morton_from_grid(q[:, 0], q[:, 1], q[:, 2]))
