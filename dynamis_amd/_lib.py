@@ -12,7 +12,9 @@ import os
 import torch  # noqa: F401  (must precede the dlopen below)
 
 _HERE = os.path.dirname(os.path.abspath(__file__))
-LIB_PATH = os.path.join(_HERE, "libdynamis_graph.so")
+# DYNAMIS_GRAPH_LIB selects another build of the same library (e.g. one compiled with
+# different options); the default is the in-tree build.
+LIB_PATH = os.environ.get("DYNAMIS_GRAPH_LIB") or os.path.join(_HERE, "libdynamis_graph.so")
 
 DG_F32, DG_F64, DG_I64, DG_I32 = 0, 1, 2, 3
 DG_OK, DG_ERR_INVALID, DG_ERR_WORKSPACE, DG_ERR_HIP, DG_ERR_RANGE, DG_ERR_CAPACITY = range(6)

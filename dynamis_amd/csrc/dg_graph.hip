@@ -260,6 +260,7 @@ struct SearchArgs {
                    // stencil rows are trimmed to the padded cutoff sphere
     float hax, hbx, hby, hcx, hcy, hcz;  // bin step vectors C[d] / nb[d] (lower triangle)
     float rprune2, pmargin;
+    float inv_hax, inv_hby, inv_hcz;  // reciprocals of the diagonal bin steps
     int nb[3], P[3], T[3], ntl[3], R[3], pbc[3];
     int tb, nregion;
     int64_t ntiles;
@@ -292,8 +293,12 @@ struct SearchArgs {
     int vout_f64;
     int64_t capacity;
     int64_t* totals;
-    uint16_t* slot;  // per-target neighbour slots (K region indices each), or null
+    // Per-target neighbour slots (K region indices each), or null.  Entries go in groups
+    // of 8 (16 bytes), group-major: group g of target j at slot + 8 * (g * nslot + j), so
+    // the groups that neighbouring targets fill at about the same time share cache lines.
+    uint16_t* slot;
     int K;
+    int64_t nslot;  // targets (group row length)
 };
 
 // Output order -> tile rank: consecutive workgroups go round-robin to the 8 XCDs, so
@@ -528,7 +533,8 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, 
             tcur = rfl(lo);
         }
         const int64_t wbase = ebase + E0;
-        const uint16_t* __restrict__ sl = a.slot + (size_t)(tbeg + k0) * a.K;
+        const char* __restrict__ sl = (const char*)a.slot + (size_t)16 * (tbeg + k0);
+        const uint32_t gstep = 16u * (uint32_t)a.nslot;  // bytes between a target's groups
 
         // Edges [b0, b1) of the batch (b1 - b0 <= 64 * kExpandIlp), lane-strided: edge
         // b0 + 64u + lane -> source id, target id, packed shift; ok = false past b1 or for
@@ -558,8 +564,10 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, 
             }
 #pragma unroll
             for (int u = 0; u < kExpandIlp; ++u) {
-                const uint32_t at = L.kk[u] < a.K ? (uint32_t)(L.tt[u] * a.K + L.kk[u]) : 0u;
-                L.raw[u] = (int)sl[at];
+                const uint32_t at = L.kk[u] < a.K ? (uint32_t)(L.kk[u] >> 3) * gstep +
+                                                        16u * (uint32_t)L.tt[u] + 2u * (L.kk[u] & 7)
+                                                  : 0u;
+                L.raw[u] = (int)*(const uint16_t*)(sl + at);
             }
             // the lane holding edge b1 - 1 has its target in t
             if (b1 > b0) tcur = __builtin_amdgcn_readlane(t, (b1 - 1 - b0) & 63);
@@ -910,7 +918,10 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         }
         const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
         // the target's position inside its bin in bin units (lower-triangular cells)
-        const float Oz = uz / a.hcz, Oy = (uy - Oz * a.hcy) / a.hby, Ox = (ux - Oy * a.hbx - Oz * a.hcx) / a.hax;
+        // (reciprocals and the hardware square root below: their few-ulp errors are far
+        // inside the trimming margin pmargin)
+        const float Oz = uz * a.inv_hcz, Oy = (uy - Oz * a.hcy) * a.inv_hby,
+                    Ox = (ux - Oy * a.hbx - Oz * a.hcx) * a.inv_hax;
 
         // Sweep this lane's target over the resident chunk c, in the fixed order (dz, dy,
         // x, atom); on_cand(v, edge, k) receives every candidate's chunk-local region index,
@@ -939,11 +950,11 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                         gz = fmaxf(gz - a.pmargin, 0.f);
                         const float rem2 = a.rprune2 - gy * gy - gz * gz;
                         if (rem2 < 0.f) continue;
-                        const float rem = sqrtf(rem2);
+                        const float rem = __builtin_amdgcn_sqrtf(rem2);
                         const float sl = fminf(py * a.hbx, (py + 1.f) * a.hbx) + fminf(pz * a.hcx, (pz + 1.f) * a.hcx);
                         const float sh = fmaxf(py * a.hbx, (py + 1.f) * a.hbx) + fmaxf(pz * a.hcx, (pz + 1.f) * a.hcx);
-                        xlo = max((int)floorf(Ox + (-rem - sh) / a.hax) + a.P[0], 0);
-                        xhi = min((int)floorf(Ox + (rem - sl) / a.hax) + a.P[0], nrx - 1);
+                        xlo = max((int)floorf(Ox + (-rem - sh) * a.inv_hax) + a.P[0], 0);
+                        xhi = min((int)floorf(Ox + (rem - sl) * a.inv_hax) + a.P[0], nrx - 1);
                     }
                     const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
                     const int va = max(sh.rt.rp[rb + xlo], c0) - c0;
@@ -963,7 +974,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                         bool e1 = in1 & (d21 < a.lo_in) & (d21 > a.tiny);
                         const bool b0 = !e0 & (d20 <= a.hi) & (v != vs);
                         const bool b1 = in1 & !e1 & (d21 <= a.hi) & (v + 1 != vs);
-                        if (__builtin_expect(__ballot(b0 | b1) != 0ull, 0)) {
+                        if (__builtin_expect(b0 | b1, 0)) {  // divergent: the mask test is scalar
                             if (b0) {
                                 const uint32_t Tp = cand_T(c0 + v);
                                 e0 = exact_edge(a, __float_as_int(q0.w), my_id, unpack3(Tp, 0) + fx,
@@ -988,24 +999,42 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             // ---------------- count pass
             uint16_t* lb = sh.lb[threadIdx.x];
             const bool slots = one_chunk && a.slot != nullptr;
-            uint16_t* myslot = a.slot + (size_t)j * a.K;
+            char* const slotb = (char*)a.slot;
+            const uint32_t gstep = 16u * (uint32_t)a.nslot;  // bytes between a target's groups
+            uint32_t goff = 16u * (uint32_t)j;                // byte offset of the next group
+            // the last full group of 8 entries and its byte offset.  Before the first
+            // group fills, pend points at the target's last group: that group is either
+            // never read (fewer than K - 7 neighbours) or written later by this lane.
+            uint4 pend = make_uint4(0, 0, 0, 0);
+            uint32_t pend_off = goff + (uint32_t)(a.K / 8 - 1) * gstep;
             for (int c = 0; c < nchunks; ++c) {
                 ensure_chunk(c);
                 if (!active) continue;
                 if (slots) {
                     sweep(c, [&](int v, bool e, int k) {
                         // the entry of slot k is written for every candidate (an edge
-                        // keeps it: k advances); 8 entries go out when an edge fills them
+                        // keeps it: k advances).  When an edge fills the 8 entries they are
+                        // read back into registers, and stored to the slot only when the
+                        // next group fills (or at the end), so the store never waits on
+                        // the read.  LDS accesses of a wave stay in program order, so the
+                        // read sees the group before the next candidate's entry lands.
                         lb[k & 7] = (uint16_t)v;
-                        if (e && (k & 7) == 7 && k < a.K) *(uint4*)(myslot + (k - 7)) = *(const uint4*)lb;
+                        if (e && (k & 7) == 7 && k < a.K) {
+                            *(uint4*)(slotb + pend_off) = pend;
+                            pend = *(const uint4*)lb;
+                            pend_off = goff;
+                            goff += gstep;
+                        }
                     });
                 } else {
                     sweep(c, [&](int, bool, int) {});
                 }
             }
             if (active) {
-                if (slots && (found & 7) && found < a.K)
-                    *(uint4*)(myslot + (found & ~7)) = *(const uint4*)lb;
+                if (slots) {
+                    *(uint4*)(slotb + pend_off) = pend;
+                    if ((found & 7) && found < a.K) *(uint4*)(slotb + goff) = *(const uint4*)lb;
+                }
                 a.cnt[j] = found;
                 if (a.counts_user) a.counts_user[caller] = found;
                 tile_found += found;
@@ -1290,6 +1319,9 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.hcx = (float)(p.C[6] / p.nb[2]);
     a.hcy = (float)(p.C[7] / p.nb[2]);
     a.hcz = (float)(p.C[8] / p.nb[2]);
+    a.inv_hax = (float)(p.nb[0] / p.C[0]);
+    a.inv_hby = (float)(p.nb[1] / p.C[4]);
+    a.inv_hcz = (float)(p.nb[2] / p.C[8]);
     // row trimming must never drop a candidate the exact test could accept: pad the
     // cutoff by far more than the fp32 position error
     a.pmargin = (float)(1e-4 * p.r + 1e-3);
@@ -1319,8 +1351,10 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.tfix = at<int>(ws, p.o_tfix);
     a.tbase = at<int64_t>(ws, p.o_tbase);
     a.totals = at<int64_t>(ws, p.o_tot);
-    a.slot = at<uint16_t>(ws, p.o_slot);
+    // slots are addressed with 32-bit byte offsets; larger problems sweep twice instead
+    a.slot = 2.0 * p.K * (double)p.nt < 4294967296.0 ? at<uint16_t>(ws, p.o_slot) : nullptr;
     a.K = p.K;
+    a.nslot = p.nt;
     return a;
 }
 
