@@ -326,10 +326,6 @@ struct ExpandStage {
     int st_dst[kBlock / 64][kStage];
     uint32_t st_S[kBlock / 64][kStage];
 };
-struct RegionTab {
-    int rp[kMaxRegion + 1];
-    int rg[kMaxRegion];
-};
 struct BatchTab {
     int off[kBlock + 1];  // edge offsets of the batch's targets
     int tid[kBlock];
@@ -337,25 +333,27 @@ struct BatchTab {
 };
 constexpr int kQBytes = (int)sizeof(float4) * (kCap + 1);
 static_assert(sizeof(ExpandStage) <= (size_t)kQBytes, "expansion view exceeds the region buffer");
-static_assert(sizeof(BatchTab) <= sizeof(RegionTab), "batch tables exceed the region table");
 
+constexpr int kRing = 16;  // slot entries a lane stages in LDS (two groups of 8)
 struct SearchLds {
     __align__(16) unsigned char qbuf[kQBytes];
-    union {
-        RegionTab rt;
-        BatchTab bt;
-    };
     int tbs[kTileMax * kTileMax * kTileMax + 1];  // bin starts of the tile
     int64_t w64[kBlock / 64];
     int w32[kBlock / 64];
     int64_t bc[2];  // workgroup broadcasts
 };
 struct CountLds : SearchLds {
-    __align__(16) uint16_t lb[kBlock][8];  // per-lane staging of 8 slot entries
+    int rp[kMaxRegion + 1];                     // first region entry of each region bin
+    __align__(16) uint16_t lb[kBlock][kRing];   // per-lane ring of slot entries
 };
 struct FixLds : SearchLds {
+    int rp[kMaxRegion + 1];
     uint32_t T[kCap + 1];  // packed (bin image shift - source floor) per entry
 };
+struct ExpandLds : SearchLds {
+    BatchTab bt;
+};
+static_assert(sizeof(CountLds) <= 40960, "count pass must fit four workgroups per CU");
 template <int MODE>
 struct LdsOf { typedef CountLds type; };
 template <>
@@ -409,38 +407,54 @@ __device__ __forceinline__ void emit_edge(const SearchArgs& a, int64_t o, int sr
     }
 }
 
-// ---------------------------------------------------------------- edge expansion
-// Cell-list range of the region bins rb = kRegPerThread * threadIdx.x + h of the tile at
-// bin g0 (periodic wrap on pbc axes; empty outside the grid on the others).
-__device__ __forceinline__ int region_bins(const SearchArgs& a, const int* g0, int* rcnt, int* rst)
+// ---------------------------------------------------------------- region bins
+// Bin-list key of region bin rb of the tile at bin g0 (periodic wrap on pbc axes); false
+// outside the grid on a non-periodic axis (an empty bin).
+__device__ __forceinline__ bool region_bin_key(const SearchArgs& a, const int* g0, int rb,
+                                               int64_t* key)
 {
     const int R0 = a.R[0], R1 = a.R[1];
+    const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
+    int w[3];
+    bool ok = true;
+#pragma unroll
+    for (int d = 0; d < 3; ++d) {
+        const int gg = g0[d] - a.P[d] + r[d];
+        if (a.pbc[d]) {
+            const int m = gg % a.nb[d];
+            w[d] = m < 0 ? m + a.nb[d] : m;
+        } else {
+            ok = ok && gg >= 0 && gg < a.nb[d];
+            w[d] = gg;
+        }
+    }
+    if (!ok) return false;
+    const int t0 = w[0] / a.T[0], t1 = w[1] / a.T[1], t2 = w[2] / a.T[2];
+    const int l0 = w[0] - t0 * a.T[0], l1 = w[1] - t1 * a.T[1], l2 = w[2] - t2 * a.T[2];
+    const int tl = t0 + a.ntl[0] * (t1 + a.ntl[1] * t2);
+    *key = (int64_t)a.rank_of_tile[tl] * a.tb + (l0 + a.T[0] * (l1 + a.T[1] * l2));
+    return true;
+}
+
+// Cell-list start of region bin rb (0 for a bin outside the grid, which is empty).
+__device__ __forceinline__ int region_bin_start(const SearchArgs& a, const int* g0, int rb)
+{
+    int64_t key;
+    return region_bin_key(a, g0, rb, &key) ? a.bstart[key] : 0;
+}
+
+// Cell-list range of the region bins rb = kRegPerThread * threadIdx.x + h of the tile at
+// bin g0; returns the thread's total.
+__device__ __forceinline__ int region_bins(const SearchArgs& a, const int* g0, int* rcnt, int* rst)
+{
     int sum = 0;
 #pragma unroll
     for (int h = 0; h < kRegPerThread; ++h) {
         rcnt[h] = 0;
         rst[h] = 0;
         const int rb = kRegPerThread * threadIdx.x + h;
-        if (rb >= a.nregion) continue;
-        const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
-        int w[3];
-        bool ok = true;
-#pragma unroll
-        for (int d = 0; d < 3; ++d) {
-            const int gg = g0[d] - a.P[d] + r[d];
-            if (a.pbc[d]) {
-                const int m = gg % a.nb[d];
-                w[d] = m < 0 ? m + a.nb[d] : m;
-            } else {
-                ok = ok && gg >= 0 && gg < a.nb[d];
-                w[d] = gg;
-            }
-        }
-        if (ok) {
-            const int t0 = w[0] / a.T[0], t1 = w[1] / a.T[1], t2 = w[2] / a.T[2];
-            const int l0 = w[0] - t0 * a.T[0], l1 = w[1] - t1 * a.T[1], l2 = w[2] - t2 * a.T[2];
-            const int tl = t0 + a.ntl[0] * (t1 + a.ntl[1] * t2);
-            const int64_t key = (int64_t)a.rank_of_tile[tl] * a.tb + (l0 + a.T[0] * (l1 + a.T[1] * l2));
+        int64_t key;
+        if (rb < a.nregion && region_bin_key(a, g0, rb, &key)) {
             rst[h] = a.bstart[key];
             rcnt[h] = a.bstart[key + 1] - rst[h];
         }
@@ -453,10 +467,11 @@ typedef float v3f __attribute__((ext_vector_type(3)));
 typedef float v4f __attribute__((ext_vector_type(4)));
 typedef int v4i __attribute__((ext_vector_type(4)));
 
+// ---------------------------------------------------------------- edge expansion
 // Stages the tile's region into ExpandStage::e as (source atom id, packed bin shift -
 // floor) pairs -- 8 bytes per entry -- bin by bin from the cell list.  The caller has
 // finished every use of the float4 view of the region buffer.
-__device__ __forceinline__ void stage_pairs(const SearchArgs& a, SearchLds& sh, const int* g0)
+__device__ __forceinline__ void stage_pairs(const SearchArgs& a, ExpandLds& sh, const int* g0)
 {
     ExpandStage& X = *(ExpandStage*)sh.qbuf;
     {
@@ -497,7 +512,7 @@ __device__ __forceinline__ void stage_pairs(const SearchArgs& a, SearchLds& sh, 
 // time, lane e finding its target by a short forward walk from the wave's current target.
 // Edges k >= K are left to search_kernel<1>.  PLAIN: no vector / distance outputs.
 template <bool PLAIN>
-__device__ __forceinline__ void expand_tile(const SearchArgs& a, SearchLds& sh, int tbeg, int ntg,
+__device__ __forceinline__ void expand_tile(const SearchArgs& a, ExpandLds& sh, int tbeg, int ntg,
                                             int64_t ebase)
 {
     ExpandStage& X = *(ExpandStage*)sh.qbuf;
@@ -778,47 +793,19 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
     // ---- region table: (T+2P)^3 bins around the tile, periodic wrap on pbc axes
     const int R0 = a.R[0], R1 = a.R[1];
     int rcnt[kRegPerThread], rst[kRegPerThread];
-    int mysum = 0;
-#pragma unroll
-    for (int h = 0; h < kRegPerThread; ++h) {
-        rcnt[h] = 0;
-        rst[h] = 0;
-        const int rb = kRegPerThread * threadIdx.x + h;
-        if (rb >= a.nregion) continue;
-        const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
-        int w[3];
-        bool ok = true;
-#pragma unroll
-        for (int d = 0; d < 3; ++d) {
-            const int gg = g0[d] - a.P[d] + r[d];
-            if (a.pbc[d]) {
-                const int m = gg % a.nb[d];
-                w[d] = m < 0 ? m + a.nb[d] : m;
-            } else {
-                ok = ok && gg >= 0 && gg < a.nb[d];
-                w[d] = gg;
-            }
-        }
-        if (ok) {
-            const int t0 = w[0] / a.T[0], t1 = w[1] / a.T[1], t2 = w[2] / a.T[2];
-            const int l0 = w[0] - t0 * a.T[0], l1 = w[1] - t1 * a.T[1], l2 = w[2] - t2 * a.T[2];
-            const int tl = t0 + a.ntl[0] * (t1 + a.ntl[1] * t2);
-            const int64_t key = (int64_t)a.rank_of_tile[tl] * a.tb + (l0 + a.T[0] * (l1 + a.T[1] * l2));
-            rst[h] = a.bstart[key];
-            rcnt[h] = a.bstart[key + 1] - rst[h];
-        }
-        mysum += rcnt[h];
-    }
+    const int mysum = region_bins(a, g0, rcnt, rst);
     int total;
+    int rex[kRegPerThread];  // first region entry of this thread's bins
     {
         int ex = block_excl_scan<int, kBlock>(mysum, sh.w32, &total);
 #pragma unroll
         for (int h = 0; h < kRegPerThread; ++h) {
             const int rb = kRegPerThread * threadIdx.x + h;
-            if (rb < a.nregion) { sh.rt.rp[rb] = ex; sh.rt.rg[rb] = rst[h]; }
+            rex[h] = ex;
+            if (rb < a.nregion) sh.rp[rb] = ex;
             ex += rcnt[h];
         }
-        if (threadIdx.x == 0) sh.rt.rp[a.nregion] = total;
+        if (threadIdx.x == 0) sh.rp[a.nregion] = total;
     }
     __syncthreads();
     const int nchunks = (total + kCap - 1) / kCap;
@@ -837,7 +824,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         }
         return pack3(sb[0] - unpack3(fl, 0), sb[1] - unpack3(fl, 1), sb[2] - unpack3(fl, 2));
     };
-    // the same for region entry vreg (count pass: no table; a search over the bin starts)
+    // the same for region entry vreg (count pass: no table; a search over the bin starts,
+    // then the bin's cell-list start from the bin key -- a rare path)
     auto cand_T = [&](int vreg) -> uint32_t {
         if constexpr (WRITE) {
             return sh.T[vreg % kCap];
@@ -845,30 +833,37 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             int lo = 0, hi = a.nregion;
             while (hi - lo > 1) {
                 const int mid = (lo + hi) >> 1;
-                if (sh.rt.rp[mid] <= vreg) lo = mid; else hi = mid;
+                if (sh.rp[mid] <= vreg) lo = mid; else hi = mid;
             }
-            return entry_T(lo, sh.rt.rg[lo] + (vreg - sh.rt.rp[lo]));
+            return entry_T(lo, region_bin_start(a, g0, lo) + (vreg - sh.rp[lo]));
         }
     };
 
+    // every thread copies the entries of its own region bins that fall in chunk c
     auto load_chunk = [&](int c) {
         const int c0 = c * kCap;
         const int c1 = min(total, c0 + kCap);
-        for (int v = threadIdx.x; v < c1 - c0; v += kBlock) {
-            const int vv = c0 + v;
-            int lo = 0, hi = a.nregion;
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (sh.rt.rp[mid] <= vv) lo = mid; else hi = mid;
-            }
-            const int rb = lo;
-            const int gidx = sh.rt.rg[rb] + (vv - sh.rt.rp[rb]);
-            const float4 e = a.spos[gidx];
+#pragma unroll
+        for (int h = 0; h < kRegPerThread; ++h) {
+            const int rb = kRegPerThread * threadIdx.x + h;
+            const int b0 = max(rex[h], c0), b1 = min(rex[h] + rcnt[h], c1);
+            if (b0 >= b1) continue;
             const int r[3] = {rb % R0, (rb / R0) % R1, rb / (R0 * R1)};
             float o[3];
             region_offset(a, r[0], r[1], r[2], o);
-            shq[v] = make_float4(e.x + o[0], e.y + o[1], e.z + o[2], e.w);
-            if constexpr (WRITE) sh.T[v] = entry_T(rb, gidx);
+            const int g = rst[h] - rex[h];  // cell-list index minus region index
+            for (int vv = b0; vv < b1; vv += 4) {
+                float4 e[4];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (vv + u < b1) e[u] = a.spos[g + vv + u];
+#pragma unroll
+                for (int u = 0; u < 4; ++u)
+                    if (vv + u < b1) {
+                        shq[vv + u - c0] = make_float4(e[u].x + o[0], e[u].y + o[1], e[u].z + o[2], e[u].w);
+                        if constexpr (WRITE) sh.T[vv + u - c0] = entry_T(rb, g + vv + u);
+                    }
+            }
         }
     };
     auto ensure_chunk = [&](int c) {  // uniform
@@ -914,7 +909,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             t0 = e.x + o[0]; t1 = e.y + o[1]; t2 = e.z + o[2];
             // the target's own region entry (same atom, zero shift) is never an edge
             const int rb_self = ((lz + a.P[2]) * R1 + (ly + a.P[1])) * R0 + (lx + a.P[0]);
-            v_self = sh.rt.rp[rb_self] + (sidx - sh.rt.rg[rb_self]);
+            const int bin_start = a.subset ? a.bstart[kb + lo] : sh.tbs[lo];
+            v_self = sh.rp[rb_self] + (sidx - bin_start);
         }
         const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
         // the target's position inside its bin in bin units (lower-triangular cells)
@@ -928,7 +924,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         // whether it is an edge, and the running neighbour number k (the edge's number when
         // it is one).
         int found = 0;
-        auto sweep = [&](int c, auto&& on_cand) {
+        auto sweep = [&](int c, auto&& on_cand, auto&& on_step, auto&& on_row) {
             const int c0 = c * kCap;
             const int c1 = min(total, c0 + kCap);
             const int vs = v_self - c0;
@@ -957,8 +953,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                         xhi = min((int)floorf(Ox + (rem - sl) * a.inv_hax) + a.P[0], nrx - 1);
                     }
                     const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
-                    const int va = max(sh.rt.rp[rb + xlo], c0) - c0;
-                    const int vb = min(sh.rt.rp[rb + xhi + 1], c1) - c0;
+                    const int va = max(sh.rp[rb + xlo], c0) - c0;
+                    const int vb = min(sh.rp[rb + xhi + 1], c1) - c0;
                     // two candidates per step, both loads issued first (the second may be
                     // one past the row -- at most the sentinel -- and is then masked); the
                     // edge test is branch-free, the rare exact test sits behind a
@@ -990,50 +986,48 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                         found += e0;
                         on_cand(v + 1, e1, found);
                         found += e1;
+                        on_step(found);
                     }
+                    on_row(found);
                 }
             }
         };
+        auto none = [](int) {};
 
         if constexpr (!WRITE) {
             // ---------------- count pass
+            // Slot entries are staged in a per-lane LDS ring of 16: the entry of slot k is
+            // written for every candidate (an edge keeps it: k advances), and full groups
+            // of 8 go out to the slot at the end of each row -- or within the row, before
+            // the ring could wrap onto a group not yet stored.
             uint16_t* lb = sh.lb[threadIdx.x];
             const bool slots = one_chunk && a.slot != nullptr;
             char* const slotb = (char*)a.slot;
             const uint32_t gstep = 16u * (uint32_t)a.nslot;  // bytes between a target's groups
-            uint32_t goff = 16u * (uint32_t)j;                // byte offset of the next group
-            // the last full group of 8 entries and its byte offset.  Before the first
-            // group fills, pend points at the target's last group: that group is either
-            // never read (fewer than K - 7 neighbours) or written later by this lane.
-            uint4 pend = make_uint4(0, 0, 0, 0);
-            uint32_t pend_off = goff + (uint32_t)(a.K / 8 - 1) * gstep;
+            uint32_t goff = 16u * (uint32_t)j;                // byte offset of group kf / 8
+            int kf = 0;                                       // entries stored (or skipped)
+            auto flush = [&](int k) {  // every full group below entry k
+                while (kf + 8 <= k) {
+                    if (kf + 8 <= a.K) *(uint4*)(slotb + goff) = *(const uint4*)(lb + (kf & 8));
+                    kf += 8;
+                    goff += gstep;
+                }
+            };
             for (int c = 0; c < nchunks; ++c) {
                 ensure_chunk(c);
                 if (!active) continue;
                 if (slots) {
-                    sweep(c, [&](int v, bool e, int k) {
-                        // the entry of slot k is written for every candidate (an edge
-                        // keeps it: k advances).  When an edge fills the 8 entries they are
-                        // read back into registers, and stored to the slot only when the
-                        // next group fills (or at the end), so the store never waits on
-                        // the read.  LDS accesses of a wave stay in program order, so the
-                        // read sees the group before the next candidate's entry lands.
-                        lb[k & 7] = (uint16_t)v;
-                        if (e && (k & 7) == 7 && k < a.K) {
-                            *(uint4*)(slotb + pend_off) = pend;
-                            pend = *(const uint4*)lb;
-                            pend_off = goff;
-                            goff += gstep;
-                        }
-                    });
+                    sweep(c, [&](int v, bool, int k) { lb[k & (kRing - 1)] = (uint16_t)v; },
+                          [&](int k) { if (k - kf > kRing - 2) flush(k); },
+                          [&](int k) { flush(k); });
                 } else {
-                    sweep(c, [&](int, bool, int) {});
+                    sweep(c, [&](int, bool, int) {}, none, none);
                 }
             }
             if (active) {
                 if (slots) {
-                    *(uint4*)(slotb + pend_off) = pend;
-                    if ((found & 7) && found < a.K) *(uint4*)(slotb + goff) = *(const uint4*)lb;
+                    flush(found);
+                    if ((found & 7) && found < a.K) *(uint4*)(slotb + goff) = *(const uint4*)(lb + (kf & 8));
                 }
                 a.cnt[j] = found;
                 if (a.counts_user) a.counts_user[caller] = found;
@@ -1052,7 +1046,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         if (one_chunk) {
             // targets with more than K neighbours: the rest by a second sweep
             const bool over = active && mycnt > a.K;
-            if (__syncthreads_or(over)) {
+            if (block_any<kBlock>(over, sh.w32)) {
                 ensure_chunk(0);
                 if (over) {
                     const int64_t base = ebase + ex;
@@ -1062,7 +1056,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                             emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
                                       unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
                         }
-                    });
+                    }, none, none);
                 }
             }
         } else {
@@ -1077,7 +1071,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                         emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
                                   unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
                     }
-                });
+                }, none, none);
             }
         }
         ebase += btot;
@@ -1088,7 +1082,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
     if (!WRITE) {
         int64_t tt;
         block_excl_scan<int64_t, kBlock>(tile_found, sh.w64, &tt);
-        const bool over = __syncthreads_or(over_any);
+        const bool over = block_any<kBlock>(over_any, sh.w32);
         const int fix = (over ? kFixOver : 0) | ((one_chunk && a.slot != nullptr) ? 0 : kFixChunked);
         out.tt = tt;
         out.fix = fix;
@@ -1113,7 +1107,7 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 // search_kernel<1>).
 __global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
 {
-    __shared__ SearchLds sh;
+    __shared__ ExpandLds sh;
     const int64_t ord = blockIdx.x;  // output order, as search_kernel
     const int64_t rank = xcd_tile_rank(ord, a.ntiles);
     const int* tstart = a.subset ? a.tbstart : a.bstart;

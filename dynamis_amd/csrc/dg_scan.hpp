@@ -43,6 +43,22 @@ __device__ __forceinline__ T block_excl_scan(T v, T* s_w, T* total)
     return before + x - v;
 }
 
+// True on every thread when v is true on any thread of the workgroup of NT threads (s_w:
+// NT/64 ints of scratch; the runtime's __syncthreads_or would add its own LDS).
+template <int NT>
+__device__ __forceinline__ bool block_any(bool v, int* s_w)
+{
+    const int w = threadIdx.x >> 6;
+    const bool wv = __builtin_amdgcn_ballot_w64(v) != 0ull;
+    if ((threadIdx.x & 63) == 0) s_w[w] = wv;
+    __syncthreads();
+    int any = 0;
+#pragma unroll
+    for (int i = 0; i < NT / 64; ++i) any |= s_w[i];
+    __syncthreads();
+    return any != 0;
+}
+
 // Phase 1: per-workgroup sums of kScanTile items.
 template <typename Tin, typename Tout>
 __global__ __launch_bounds__(kScanBlock) void scan_reduce_kernel(const Tin* __restrict__ in,
