@@ -920,76 +920,104 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                     Ox = (ux - Oy * a.hbx - Oz * a.hcx) * a.inv_hax;
 
         // Sweep this lane's target over the resident chunk c, in the fixed order (dz, dy,
-        // x, atom); on_cand(v, edge, k) receives every candidate's chunk-local region index,
-        // whether it is an edge, and the running neighbour number k (the edge's number when
-        // it is one).
+        // x, atom) -- ascending region index; on_cand(v, edge, k) receives every candidate's
+        // chunk-local region index, whether it is an edge, and the running neighbour number
+        // k (the edge's number when it is one); on_step(k) follows every step of two
+        // candidates, on_row(k) every row.
+        //
+        // Rows are swept with one row of lookahead: the wave stays on row r until every
+        // lane has finished its row r, and a lane that finishes early goes on into its row
+        // r + 1 meanwhile, so a wave waits for its longest row less often.
         int found = 0;
+        // candidate range [va, vb) of row ri (oz * nry + oy) of this lane, chunk-local;
+        // empty when the padded cutoff sphere misses the row
+        auto row_range = [&](int ri, int c0, int c1, int& va, int& vb) {
+            const int oz = ri / nry, oy = ri - oz * nry;
+            int xlo = 0, xhi = nrx - 1;
+            va = vb = 0;
+            if (a.lowtri) {
+                // bounding box of the row (bins py, pz relative to the target's bin, all x)
+                // in Cartesian y and z, from the target: its gaps gy, gz bound the distance
+                // from below; the x range that the (padded) cutoff sphere can reach then
+                // follows from the row's x shear
+                const float py = (float)(oy - a.P[1]) - Oy, pz = (float)(oz - a.P[2]) - Oz;
+                const float zl = pz * a.hcz, zh = zl + a.hcz;
+                const float cyl = fminf(pz * a.hcy, (pz + 1.f) * a.hcy);
+                const float cyh = fmaxf(pz * a.hcy, (pz + 1.f) * a.hcy);
+                const float yl = py * a.hby + cyl, yh = (py + 1.f) * a.hby + cyh;
+                float gy = fmaxf(fmaxf(yl, -yh), 0.f), gz = fmaxf(fmaxf(zl, -zh), 0.f);
+                gy = fmaxf(gy - a.pmargin, 0.f);
+                gz = fmaxf(gz - a.pmargin, 0.f);
+                const float rem2 = a.rprune2 - gy * gy - gz * gz;
+                if (rem2 < 0.f) return;
+                const float rem = __builtin_amdgcn_sqrtf(rem2);
+                const float sl = fminf(py * a.hbx, (py + 1.f) * a.hbx) + fminf(pz * a.hcx, (pz + 1.f) * a.hcx);
+                const float sh = fmaxf(py * a.hbx, (py + 1.f) * a.hbx) + fmaxf(pz * a.hcx, (pz + 1.f) * a.hcx);
+                xlo = max((int)floorf(Ox + (-rem - sh) * a.inv_hax) + a.P[0], 0);
+                xhi = min((int)floorf(Ox + (rem - sl) * a.inv_hax) + a.P[0], nrx - 1);
+                if (xlo > xhi) return;
+            }
+            const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
+            va = max(sh.rp[rb + xlo], c0) - c0;
+            vb = min(sh.rp[rb + xhi + 1], c1) - c0;
+            if (va >= vb) va = vb = 0;
+        };
         auto sweep = [&](int c, auto&& on_cand, auto&& on_step, auto&& on_row) {
             const int c0 = c * kCap;
             const int c1 = min(total, c0 + kCap);
             const int vs = v_self - c0;
-            for (int oz = 0; oz < nrz; ++oz) {
-                for (int oy = 0; oy < nry; ++oy) {
-                    int xlo = 0, xhi = nrx - 1;
-                    if (a.lowtri) {
-                        // bounding box of the row (bins py, pz relative to the target's bin,
-                        // all x) in Cartesian y and z, from the target: its gaps gy, gz bound
-                        // the distance from below; the x range that the (padded) cutoff sphere
-                        // can reach then follows from the row's x shear
-                        const float py = (float)(oy - a.P[1]) - Oy, pz = (float)(oz - a.P[2]) - Oz;
-                        const float zl = pz * a.hcz, zh = zl + a.hcz;
-                        const float cyl = fminf(pz * a.hcy, (pz + 1.f) * a.hcy);
-                        const float cyh = fmaxf(pz * a.hcy, (pz + 1.f) * a.hcy);
-                        const float yl = py * a.hby + cyl, yh = (py + 1.f) * a.hby + cyh;
-                        float gy = fmaxf(fmaxf(yl, -yh), 0.f), gz = fmaxf(fmaxf(zl, -zh), 0.f);
-                        gy = fmaxf(gy - a.pmargin, 0.f);
-                        gz = fmaxf(gz - a.pmargin, 0.f);
-                        const float rem2 = a.rprune2 - gy * gy - gz * gz;
-                        if (rem2 < 0.f) continue;
-                        const float rem = __builtin_amdgcn_sqrtf(rem2);
-                        const float sl = fminf(py * a.hbx, (py + 1.f) * a.hbx) + fminf(pz * a.hcx, (pz + 1.f) * a.hcx);
-                        const float sh = fmaxf(py * a.hbx, (py + 1.f) * a.hbx) + fmaxf(pz * a.hcx, (pz + 1.f) * a.hcx);
-                        xlo = max((int)floorf(Ox + (-rem - sh) * a.inv_hax) + a.P[0], 0);
-                        xhi = min((int)floorf(Ox + (rem - sl) * a.inv_hax) + a.P[0], nrx - 1);
-                    }
-                    const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
-                    const int va = max(sh.rp[rb + xlo], c0) - c0;
-                    const int vb = min(sh.rp[rb + xhi + 1], c1) - c0;
-                    // two candidates per step, both loads issued first (the second may be
-                    // one past the row -- at most the sentinel -- and is then masked); the
-                    // edge test is branch-free, the rare exact test sits behind a
-                    // wave-uniform check, and on_cand sees every candidate in order
-                    for (int v = va; v < vb; v += 2) {
-                        const float4 q0 = shq[v], q1 = shq[v + 1];
-                        const bool in1 = v + 1 < vb;
-                        float dx = q0.x - t0, dyv = q0.y - t1, dzv = q0.z - t2;
-                        const float d20 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
-                        dx = q1.x - t0; dyv = q1.y - t1; dzv = q1.z - t2;
-                        const float d21 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
-                        bool e0 = (d20 < a.lo_in) & (d20 > a.tiny);
-                        bool e1 = in1 & (d21 < a.lo_in) & (d21 > a.tiny);
-                        const bool b0 = !e0 & (d20 <= a.hi) & (v != vs);
-                        const bool b1 = in1 & !e1 & (d21 <= a.hi) & (v + 1 != vs);
-                        if (__builtin_expect(b0 | b1, 0)) {  // divergent: the mask test is scalar
-                            if (b0) {
-                                const uint32_t Tp = cand_T(c0 + v);
-                                e0 = exact_edge(a, __float_as_int(q0.w), my_id, unpack3(Tp, 0) + fx,
-                                                unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
-                            }
-                            if (b1) {
-                                const uint32_t Tp = cand_T(c0 + v + 1);
-                                e1 = exact_edge(a, __float_as_int(q1.w), my_id, unpack3(Tp, 0) + fx,
-                                                unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
-                            }
+            const int nrows = nrz * nry;
+            // [v, e): this lane's unswept part of its current row (row cur); [pv, pe): its
+            // next row.  A lane moves on to its next row the step it finishes its current
+            // one, so when the wave leaves row ri every lane is on its row ri + 1.
+            int v, e, pv = 0, pe = 0, cur = 0;
+            row_range(0, c0, c1, v, e);
+            if (!active) v = e = 0;
+            for (int ri = 0; ri < nrows; ++ri) {
+                pv = pe = 0;  // (the last row has no next row)
+                if (ri + 1 < nrows && active) row_range(ri + 1, c0, c1, pv, pe);
+                if (v >= e) { v = pv; e = pe; cur = ri + 1; }  // nothing left of row ri
+                // two candidates per step, both loads issued first (the second may be one
+                // past the range -- at most the sentinel -- and is then masked); the edge
+                // test is branch-free, the rare exact test sits behind a scalar mask test,
+                // and on_cand sees every candidate in order
+                if (__builtin_amdgcn_ballot_w64(cur == ri) != 0ull) do {
+                    const float4 q0 = shq[v], q1 = shq[v + 1];
+                    const bool in0 = v < e, in1 = v + 1 < e;
+                    float dx = q0.x - t0, dyv = q0.y - t1, dzv = q0.z - t2;
+                    const float d20 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
+                    dx = q1.x - t0; dyv = q1.y - t1; dzv = q1.z - t2;
+                    const float d21 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
+                    bool e0 = in0 & (d20 < a.lo_in) & (d20 > a.tiny);
+                    bool e1 = in1 & (d21 < a.lo_in) & (d21 > a.tiny);
+                    const bool b0 = in0 & !e0 & (d20 <= a.hi) & (v != vs);
+                    const bool b1 = in1 & !e1 & (d21 <= a.hi) & (v + 1 != vs);
+                    if (__builtin_expect(b0 | b1, 0)) {  // divergent: the mask test is scalar
+                        if (b0) {
+                            const uint32_t Tp = cand_T(c0 + v);
+                            e0 = exact_edge(a, __float_as_int(q0.w), my_id, unpack3(Tp, 0) + fx,
+                                            unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
                         }
-                        on_cand(v, e0, found);
-                        found += e0;
-                        on_cand(v + 1, e1, found);
-                        found += e1;
-                        on_step(found);
+                        if (b1) {
+                            const uint32_t Tp = cand_T(c0 + v + 1);
+                            e1 = exact_edge(a, __float_as_int(q1.w), my_id, unpack3(Tp, 0) + fx,
+                                            unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
+                        }
                     }
-                    on_row(found);
-                }
+                    // (a candidate past the range is no edge: k does not advance)
+                    on_cand(v, e0, found);
+                    found += e0;
+                    on_cand(v + 1, e1, found);
+                    found += e1;
+                    on_step(found);
+                    // range done: from row ri on to the next row, from that one to rest
+                    v += 2;
+                    const bool fin = v >= e, sw = fin & (cur == ri);
+                    v = fin ? (sw ? pv : 0) : v;
+                    e = fin ? (sw ? pe : 0) : e;
+                    cur = sw ? ri + 1 : cur;
+                } while (__builtin_amdgcn_ballot_w64(cur == ri) != 0ull);
+                on_row(found);
             }
         };
         auto none = [](int) {};
@@ -1018,7 +1046,19 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 if (!active) continue;
                 if (slots) {
                     sweep(c, [&](int v, bool, int k) { lb[k & (kRing - 1)] = (uint16_t)v; },
-                          [&](int k) { if (k - kf > kRing - 2) flush(k); },
+                          [&](int k) {
+                              // k - kf <= 16 here: at most two groups to store
+                              if (k - kf > kRing - 2) {
+                                  if (kf + 8 <= a.K) *(uint4*)(slotb + goff) = *(const uint4*)(lb + (kf & 8));
+                                  kf += 8;
+                                  goff += gstep;
+                                  if (k - kf >= 8) {
+                                      if (kf + 8 <= a.K) *(uint4*)(slotb + goff) = *(const uint4*)(lb + (kf & 8));
+                                      kf += 8;
+                                      goff += gstep;
+                                  }
+                              }
+                          },
                           [&](int k) { flush(k); });
                 } else {
                     sweep(c, [&](int, bool, int) {}, none, none);
