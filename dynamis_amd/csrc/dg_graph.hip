@@ -254,6 +254,7 @@ __global__ void finish_targets_kernel(int64_t nbins, int64_t n, const int* __res
 // ---------------------------------------------------------------- neighbour search
 struct SearchArgs {
     double C[9];
+    double Cinv[9];
     double hC[9];  // bin step vectors: row d = C[d] / nb[d]
     double r2;
     int lowtri;    // lower-triangular cell (a along x, b in the xy plane, positive diagonal):
@@ -359,23 +360,34 @@ struct LdsOf { typedef CountLds type; };
 template <>
 struct LdsOf<1> { typedef FixLds type; };
 
+// Cartesian offset of region bin (rx, ry, rz) from the centre of its tile: positions in
+// LDS are relative to the tile centre, which keeps their magnitudes (and so their
+// rounding) small.
 __device__ __forceinline__ void region_offset(const SearchArgs& a, int rx, int ry, int rz,
                                               float* o)
 {
-    const double u0 = (double)(rx - a.P[0]), u1 = (double)(ry - a.P[1]), u2 = (double)(rz - a.P[2]);
+    const double u0 = (double)(rx - a.P[0]) - 0.5 * a.T[0], u1 = (double)(ry - a.P[1]) - 0.5 * a.T[1],
+                 u2 = (double)(rz - a.P[2]) - 0.5 * a.T[2];
 #pragma unroll
     for (int c = 0; c < 3; ++c) o[c] = (float)fma(u2, a.hC[6 + c], fma(u1, a.hC[3 + c], u0 * a.hC[c]));
 }
 
-// Exact (canonical fp64) decision for a candidate the fp32 prefilter cannot settle.
-__device__ __forceinline__ bool exact_edge(const SearchArgs& a, int src, int tgt, int S0, int S1,
-                                        int S2)
+// Exact (canonical fp64) decision for a candidate the fp32 prefilter cannot settle: atom
+// src as seen from target tgt, (dq0, dq1, dq2) = its fp32 LDS position minus the target's.
+// The integer image shift is recovered by rounding: dq - (pos[src] - pos[tgt]) is S.C up
+// to the LDS rounding (~1e-5 A), far below half a cell.
+__device__ __forceinline__ bool exact_edge(const SearchArgs& a, int src, int tgt, double dq0,
+                                        double dq1, double dq2)
 {
-    if (src == tgt && S0 == 0 && S1 == 0 && S2 == 0) return false;
     double ps[3], pt[3], v[3];
     load_pos(a.pos, a.f64, src, ps);
     load_pos(a.pos, a.f64, tgt, pt);
-    double d2 = canon_d2(ps, pt, S0, S1, S2, a.C, v);
+    const double w0 = dq0 - (ps[0] - pt[0]), w1 = dq1 - (ps[1] - pt[1]), w2 = dq2 - (ps[2] - pt[2]);
+    const int S0 = (int)rint(canon_frac(w0, w1, w2, a.Cinv, 0));
+    const int S1 = (int)rint(canon_frac(w0, w1, w2, a.Cinv, 1));
+    const int S2 = (int)rint(canon_frac(w0, w1, w2, a.Cinv, 2));
+    if (src == tgt && S0 == 0 && S1 == 0 && S2 == 0) return false;
+    const double d2 = canon_d2(ps, pt, S0, S1, S2, a.C, v);
     return d2 > kSelfThr && d2 <= a.r2;
 }
 
@@ -824,21 +836,6 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         }
         return pack3(sb[0] - unpack3(fl, 0), sb[1] - unpack3(fl, 1), sb[2] - unpack3(fl, 2));
     };
-    // the same for region entry vreg (count pass: no table; a search over the bin starts,
-    // then the bin's cell-list start from the bin key -- a rare path)
-    auto cand_T = [&](int vreg) -> uint32_t {
-        if constexpr (WRITE) {
-            return sh.T[vreg % kCap];
-        } else {
-            int lo = 0, hi = a.nregion;
-            while (hi - lo > 1) {
-                const int mid = (lo + hi) >> 1;
-                if (sh.rp[mid] <= vreg) lo = mid; else hi = mid;
-            }
-            return entry_T(lo, region_bin_start(a, g0, lo) + (vreg - sh.rp[lo]));
-        }
-    };
-
     // every thread copies the entries of its own region bins that fall in chunk c
     auto load_chunk = [&](int c) {
         const int c0 = c * kCap;
@@ -921,14 +918,14 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
 
         // Sweep this lane's target over the resident chunk c, in the fixed order (dz, dy,
         // x, atom) -- ascending region index; on_cand(v, edge, k) receives every candidate's
-        // chunk-local region index, whether it is an edge, and the running neighbour number
-        // k (the edge's number when it is one); on_step(k) follows every step of two
-        // candidates, on_row(k) every row.
+        // chunk-local region index, whether it is an edge, and twice the running neighbour
+        // number, k2 = 2 k (k: the edge's number when it is one); on_step(k2) follows every
+        // step of two candidates, on_row(k2) every row.
         //
         // Rows are swept with one row of lookahead: the wave stays on row r until every
         // lane has finished its row r, and a lane that finishes early goes on into its row
         // r + 1 meanwhile, so a wave waits for its longest row less often.
-        int found = 0;
+        int found2 = 0;  // twice the neighbours found so far
         // candidate range [va, vb) of row ri (oz * nry + oy) of this lane, chunk-local;
         // empty when the padded cutoff sphere misses the row
         auto row_range = [&](int ri, int c0, int c1, int& va, int& vb) {
@@ -993,31 +990,28 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                     const bool b0 = in0 & !e0 & (d20 <= a.hi) & (v != vs);
                     const bool b1 = in1 & !e1 & (d21 <= a.hi) & (v + 1 != vs);
                     if (__builtin_expect(b0 | b1, 0)) {  // divergent: the mask test is scalar
-                        if (b0) {
-                            const uint32_t Tp = cand_T(c0 + v);
-                            e0 = exact_edge(a, __float_as_int(q0.w), my_id, unpack3(Tp, 0) + fx,
-                                            unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
-                        }
-                        if (b1) {
-                            const uint32_t Tp = cand_T(c0 + v + 1);
-                            e1 = exact_edge(a, __float_as_int(q1.w), my_id, unpack3(Tp, 0) + fx,
-                                            unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
-                        }
+                        if (b0)
+                            e0 = exact_edge(a, __float_as_int(q0.w), my_id, (double)q0.x - t0,
+                                            (double)q0.y - t1, (double)q0.z - t2);
+                        if (b1)
+                            e1 = exact_edge(a, __float_as_int(q1.w), my_id, (double)q1.x - t0,
+                                            (double)q1.y - t1, (double)q1.z - t2);
                     }
                     // (a candidate past the range is no edge: k does not advance)
-                    on_cand(v, e0, found);
-                    found += e0;
-                    on_cand(v + 1, e1, found);
-                    found += e1;
-                    on_step(found);
-                    // range done: from row ri on to the next row, from that one to rest
-                    v += 2;
-                    const bool fin = v >= e, sw = fin & (cur == ri);
-                    v = fin ? (sw ? pv : 0) : v;
-                    e = fin ? (sw ? pe : 0) : e;
+                    on_cand(v, e0, found2);
+                    found2 += e0 ? 2 : 0;
+                    on_cand(v + 1, e1, found2);
+                    found2 += e1 ? 2 : 0;
+                    on_step(found2);
+                    // range done: from row ri on to the next row, from that one to rest (at
+                    // v = e: masked loads of entries e and e + 1, inside LDS)
+                    const int nv = v + 2;
+                    const bool fin = nv >= e, sw = fin & (cur == ri);
+                    v = fin ? (sw ? pv : e) : nv;
+                    e = sw ? pe : e;
                     cur = sw ? ri + 1 : cur;
                 } while (__builtin_amdgcn_ballot_w64(cur == ri) != 0ull);
-                on_row(found);
+                on_row(found2);
             }
         };
         auto none = [](int) {};
@@ -1029,45 +1023,43 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             // of 8 go out to the slot at the end of each row -- or within the row, before
             // the ring could wrap onto a group not yet stored.
             uint16_t* lb = sh.lb[threadIdx.x];
+            char* const lbb = (char*)lb;
             const bool slots = one_chunk && a.slot != nullptr;
             char* const slotb = (char*)a.slot;
             const uint32_t gstep = 16u * (uint32_t)a.nslot;  // bytes between a target's groups
-            uint32_t goff = 16u * (uint32_t)j;                // byte offset of group kf / 8
-            int kf = 0;                                       // entries stored (or skipped)
-            auto flush = [&](int k) {  // every full group below entry k
-                while (kf + 8 <= k) {
-                    if (kf + 8 <= a.K) *(uint4*)(slotb + goff) = *(const uint4*)(lb + (kf & 8));
-                    kf += 8;
-                    goff += gstep;
-                }
+            uint32_t goff = 16u * (uint32_t)j;                // byte offset of group kf2 / 16
+            int kf2 = 0;                                      // 2 x entries stored (or skipped)
+            const int K2 = 2 * a.K;
+            auto store_group = [&]() {  // the group starting at entry kf2 / 2
+                if (kf2 + 16 <= K2) *(uint4*)(slotb + goff) = *(const uint4*)(lbb + (kf2 & 16));
+                kf2 += 16;
+                goff += gstep;
+            };
+            auto flush = [&](int k2) {  // every full group below entry k2 / 2
+                while (kf2 + 16 <= k2) store_group();
             };
             for (int c = 0; c < nchunks; ++c) {
                 ensure_chunk(c);
                 if (!active) continue;
                 if (slots) {
-                    sweep(c, [&](int v, bool, int k) { lb[k & (kRing - 1)] = (uint16_t)v; },
-                          [&](int k) {
-                              // k - kf <= 16 here: at most two groups to store
-                              if (k - kf > kRing - 2) {
-                                  if (kf + 8 <= a.K) *(uint4*)(slotb + goff) = *(const uint4*)(lb + (kf & 8));
-                                  kf += 8;
-                                  goff += gstep;
-                                  if (k - kf >= 8) {
-                                      if (kf + 8 <= a.K) *(uint4*)(slotb + goff) = *(const uint4*)(lb + (kf & 8));
-                                      kf += 8;
-                                      goff += gstep;
-                                  }
+                    sweep(c, [&](int v, bool, int k2) { *(uint16_t*)(lbb + (k2 & (2 * kRing - 2))) = (uint16_t)v; },
+                          [&](int k2) {
+                              // k2 - kf2 <= 32 here: at most two groups to store
+                              if (k2 - kf2 > 2 * kRing - 4) {
+                                  store_group();
+                                  if (k2 - kf2 >= 16) store_group();
                               }
                           },
-                          [&](int k) { flush(k); });
+                          [&](int k2) { flush(k2); });
                 } else {
                     sweep(c, [&](int, bool, int) {}, none, none);
                 }
             }
+            const int found = found2 >> 1;
             if (active) {
                 if (slots) {
-                    flush(found);
-                    if ((found & 7) && found < a.K) *(uint4*)(slotb + goff) = *(const uint4*)(lb + (kf & 8));
+                    flush(found2);
+                    if ((found & 7) && found < a.K) *(uint4*)(slotb + goff) = *(const uint4*)(lbb + (kf2 & 16));
                 }
                 a.cnt[j] = found;
                 if (a.counts_user) a.counts_user[caller] = found;
@@ -1090,7 +1082,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 ensure_chunk(0);
                 if (over) {
                     const int64_t base = ebase + ex;
-                    sweep(0, [&](int v, bool e, int k) {
+                    sweep(0, [&](int v, bool e, int k2) {
+                        const int k = k2 >> 1;
                         if (e && k >= a.K && k < mycnt) {
                             const uint32_t Tp = sh.T[v];
                             emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
@@ -1105,7 +1098,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             for (int c = 0; c < nchunks; ++c) {
                 ensure_chunk(c);
                 if (!active) continue;
-                sweep(c, [&](int v, bool e, int k) {
+                sweep(c, [&](int v, bool e, int k2) {
+                    const int k = k2 >> 1;
                     if (e && k < mycnt) {
                         const uint32_t Tp = sh.T[v];
                         emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
@@ -1342,6 +1336,7 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     SearchArgs a;
     memset(&a, 0, sizeof a);
     memcpy(a.C, p.C, sizeof a.C);
+    memcpy(a.Cinv, p.Cinv, sizeof a.Cinv);
     for (int d = 0; d < 3; ++d)
         for (int c = 0; c < 3; ++c) a.hC[3 * d + c] = p.C[3 * d + c] / (double)p.nb[d];
     a.r2 = p.r2;

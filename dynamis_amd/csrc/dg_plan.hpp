@@ -139,18 +139,36 @@ inline void plan_grid(Plan& p)
     p.nbins = p.ntiles * p.tb;
     p.ncodes = (int64_t)1 << (p.mb[0] + p.mb[1] + p.mb[2]);
 
-    // fp32 prefilter band.  Positions in LDS are fp32 offsets from the tile origin:
-    // (position - bin origin) rounded once, plus (bin origin - tile origin) rounded once.
-    // delta bounds the per-component error of the fp32 difference vector.
+    // fp32 prefilter band.  Positions in LDS are fp32 offsets from the tile centre: q =
+    // fl(rel + o), rel = (position - bin origin) rounded once, o = (bin origin - tile
+    // centre) rounded once; the same for the target t.  Every such offset lies in the box
+    // of +-m_d = T_d / 2 + P_d bins along the lattice vectors around the centre, whose
+    // largest norm (at a corner) is rmax.  Per component the fp32 difference fl(q - t)
+    // then differs from the exact canonical vector by at most
+    //   u (|rel_q| + |o_q| + |q| + |rel_t| + |o_t| + |t| + |q - t|)
+    //     <= u (2 bin_diag + 4 rmax + rr);
+    // delta takes twice that.
     const double u = 1.0 / 16777216.0;  // 2^-24
-    double len[3], bin_diag = 0, reg_diag = 0;
+    double len[3], bin_diag = 0;
     for (int d = 0; d < 3; d++) {
         len[d] = sqrt(p.C[3 * d] * p.C[3 * d] + p.C[3 * d + 1] * p.C[3 * d + 1] +
                       p.C[3 * d + 2] * p.C[3 * d + 2]);
         bin_diag += len[d] / p.nb[d];
-        reg_diag += len[d] * (double)p.R[d] / p.nb[d];
     }
-    double delta = 8.0 * u * (bin_diag + reg_diag + p.r);
+    double rmax2 = 0;
+    for (int sx = -1; sx <= 1; sx += 2)
+        for (int sy = -1; sy <= 1; sy += 2)
+            for (int sz = -1; sz <= 1; sz += 2) {
+                const int sg[3] = {sx, sy, sz};
+                double x[3] = {0, 0, 0};
+                for (int d = 0; d < 3; d++) {
+                    const double m = 0.5 * p.T[d] + p.P[d];
+                    for (int c = 0; c < 3; c++) x[c] += sg[d] * m * p.C[3 * d + c] / p.nb[d];
+                }
+                rmax2 = std::max(rmax2, x[0] * x[0] + x[1] * x[1] + x[2] * x[2]);
+            }
+    const double rmax = sqrt(rmax2);
+    double delta = 2.0 * u * (2.0 * bin_diag + 4.0 * rmax + p.r + 1.0);
     double rr = p.r + 2.0 * delta;
     double band = 2.0 * (2.0 * sqrt(3.0) * rr * delta + 3.0 * delta * delta + 4.0 * u * rr * rr);
     p.hi = nextafterf((float)(p.r2 + band), INFINITY);
