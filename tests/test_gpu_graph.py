@@ -244,3 +244,34 @@ def test_filter_edges_to_radius(cuda):
                                co.cpu().numpy().astype(np.int32))
     assert np.array_equal(ef.cpu().numpy(), ei.cpu().numpy()[:, keep])
     assert cf.dtype == co.dtype
+
+
+# ---- prefilter band: pairs within a few ulp of the cutoff ---------------------------
+def _near_cutoff_box(cell, r, n_anchor, seed, dtype):
+    """Anchors spread over the cell (many near its faces, so pairs cross the periodic
+    boundary), each with partners at r (1 + eps) in random directions, eps down to the
+    fp32 rounding of the coordinates: every such pair sits in or next to the fp32
+    prefilter band, where only the exact canonical test may decide."""
+    rng = np.random.default_rng(seed)
+    cell = np.asarray(cell, np.float64)
+    f = rng.uniform(0, 1, (n_anchor, 3))
+    h = n_anchor // 2  # these get one fractional coordinate within 2 % of a face
+    axis = rng.integers(0, 3, h)
+    f[np.arange(h), axis] = np.where(rng.uniform(size=h) < 0.5, rng.uniform(0, 0.02, h), rng.uniform(0.98, 1.0, h))
+    anchors = f @ cell
+    eps = np.array([-3e-6, -1e-6, -3e-7, -1e-7, 0.0, 1e-7, 3e-7, 1e-6, 3e-6])
+    d = rng.normal(size=(n_anchor, len(eps), 3))
+    d /= np.linalg.norm(d, axis=-1, keepdims=True)
+    partners = anchors[:, None, :] + d * (r * (1.0 + eps))[None, :, None]
+    return np.concatenate([anchors, partners.reshape(-1, 3)]).astype(dtype)
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape", ["cubic", "lowtri", "general"])
+def test_near_cutoff_pairs(cuda, dtype, shape):
+    cell = {"cubic": np.eye(3) * 215.443,
+            "lowtri": np.array([[120.0, 0, 0], [30.0, 110.0, 0], [-20.0, 25.0, 100.0]]),
+            "general": np.array([[110.0, 8.0, -5.0], [20.0, 105.0, 6.0], [-10.0, 15.0, 98.0]])}[shape]
+    pos = _near_cutoff_box(cell, 6.0, 1500, 17, dtype)
+    _, _, cnt, o = check_parity(pos, cell, (1, 1, 1), 6.0, cuda, name=f"near-cutoff {shape}")
+    assert len(o["src"]) > 1500 * 4  # the inside half of every anchor's partners at least
