@@ -36,6 +36,12 @@ def main():
     ap.add_argument("--config", default="C3")
     ap.add_argument("--no-cpu", action="store_true")
     ap.add_argument("--cpu-threads", type=int, default=0)
+    ap.add_argument("--trajectory", type=int, default=-1,
+                    help="rebuild from this many position frames, each the previous one displaced "
+                         "by Gaussian --sigma per coordinate, cycled over the steps (all resident in "
+                         "HBM before the timed region); 0 = the same positions every step.  "
+                         "Default: 100 for C5 (its stated 100 rebuilds at 0.01 A per step), else 0")
+    ap.add_argument("--sigma", type=float, default=0.01)
     ap.add_argument("--path", default="graph", choices=["graph", "halo"],
                     help="graph: the headline full rebuild; halo: extract_halo_info of one rank "
                          "of an 8-way SFC partition of the same box (edges at r + 0.5)")
@@ -101,19 +107,31 @@ def main():
     dst = torch.empty(cap, dtype=torch.int64, device=dev)
     shift = torch.empty((cap, 3), dtype=torch.float32, device=dev)
 
-    def step(ev=None):
+    # position frames: a random walk of sigma per coordinate per frame (seeded), generated
+    # on the device before any timing
+    nframes = args.trajectory if args.trajectory >= 0 else (100 if args.config == "C5" else 0)
+    frames = [pos]
+    if nframes > 1:
+        g = torch.Generator(device=dev).manual_seed(7)
+        for _ in range(nframes - 1):
+            frames.append(frames[-1] + args.sigma * torch.randn(pos.shape, generator=g, device=dev,
+                                                                dtype=pos.dtype))
+    torch.cuda.synchronize()
+
+    def step(ev=None, k=0):
         # one full rebuild = dg_graph_build: the count stage (SFC reorder, degrees, tile
         # offsets) then the write stage, back to back, no host sync
-        L.check(lib.dg_graph_count(d, L.ptr(pos), L.ptr(tgt), L.ptr(ws), wsb, L.ptr(counts), s), "count")
+        p = frames[k % len(frames)]
+        L.check(lib.dg_graph_count(d, L.ptr(p), L.ptr(tgt), L.ptr(ws), wsb, L.ptr(counts), s), "count")
         if ev is not None:
             ev[0].record(stream)
-        L.check(lib.dg_graph_write(d, L.ptr(pos), L.ptr(tgt), L.ptr(ws), wsb, cap, L.ptr(src), L.ptr(dst),
+        L.check(lib.dg_graph_write(d, L.ptr(p), L.ptr(tgt), L.ptr(ws), wsb, cap, L.ptr(src), L.ptr(dst),
                                    L.ptr(shift), None, None, 0, s), "write")
         if ev is not None:
             ev[1].record(stream)
 
-    for _ in range(args.warmup):
-        step()
+    for w in range(args.warmup):
+        step(k=w)
     torch.cuda.synchronize()
     kev = [(torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True))
            for _ in range(args.steps)]
@@ -122,14 +140,23 @@ def main():
     torch.cuda.synchronize()
     t0.record(stream)
     for k in range(args.steps):
-        step(kev[k])
+        step(kev[k], k)
     t1.record(stream)
     torch.cuda.synchronize()
     total_ms = t0.elapsed_time(t1)
     write_ms = float(np.mean([a.elapsed_time(b) for a, b in kev]))
     E = L._i64(0)
     L.check(lib.dg_graph_read_totals(d, L.ptr(ws), E, fl, s), "totals")
-    E = int(E.value)
+    E = int(E.value)  # of the last frame built
+    if len(frames) > 1:
+        # edges per rebuild over the frames timed (they differ slightly along the walk)
+        Es = []
+        for k in range(args.steps):
+            step(None, k)
+            Ek = L._i64(0)
+            L.check(lib.dg_graph_read_totals(d, L.ptr(ws), Ek, fl, s), "totals")
+            Es.append(int(Ek.value))
+        E = int(round(float(np.mean(Es))))
     ms = total_ms / args.steps
 
     # drop-in Python API (exact-size outputs, one host sync per build)
@@ -199,7 +226,9 @@ def main():
         "scaling": "weak",
         "vs_baseline": None,
         "dtype": "fp32 positions, fp64 predicate, int64 edges",
-        "data": "synthetic (seeded numpy uniform box)",
+        "data": "synthetic (seeded numpy uniform box)" + (
+            f"; {len(frames)} position frames, each displaced by Gaussian sigma={args.sigma} A per "
+            "coordinate from the previous, cycled" if len(frames) > 1 else ""),
         "config": {"workload": f"{args.config}: {box.name} N={n} r_cut={box.radius} "
                                f"pbc={list(box.pbc)}", "atoms": n, "edges": E,
                    "parallelism": "single GPU"},
