@@ -74,27 +74,41 @@ struct GridArgs {
 };
 
 // ---------------------------------------------------------------- tile SFC ranks
-__global__ void tile_flags_kernel(GridArgs g, int64_t ncodes, int* __restrict__ flag)
+// Rank of every tile in the compact Morton order (morton_encode) among the tiles of the
+// grid, computed directly: for each 1 bit of the tile's code, the tiles whose codes share
+// the bits above it and have a 0 there all come first; per axis, their coordinate has its
+// high bits fixed and f free low bits, so the axis admits clamp(n - lo, 0, 2^f) values.
+// Also clears the bin counts (bcnt) for the binning that follows.
+__global__ void tile_rank_kernel(GridArgs g, int64_t ntiles, int* __restrict__ tile_of_rank,
+                                 int* __restrict__ rank_of_tile, int* __restrict__ bcnt,
+                                 int64_t nbins)
 {
-    int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= ncodes) return;
-    int x, y, z;
-    morton_decode((uint32_t)c, g.mb, &x, &y, &z);
-    flag[c] = (x < g.ntl[0] && y < g.ntl[1] && z < g.ntl[2]) ? 1 : 0;
-}
-
-__global__ void tile_fill_kernel(GridArgs g, int64_t ncodes, const int* __restrict__ flag,
-                                 const int* __restrict__ cpos, int* __restrict__ tile_of_rank,
-                                 int* __restrict__ rank_of_tile)
-{
-    int64_t c = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (c >= ncodes || !flag[c]) return;
-    int x, y, z;
-    morton_decode((uint32_t)c, g.mb, &x, &y, &z);
-    int lin = x + g.ntl[0] * (y + g.ntl[1] * z);
-    int r = cpos[c];
-    tile_of_rank[r] = lin;
-    rank_of_tile[lin] = r;
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < nbins; q += stride) bcnt[q] = 0;
+    for (int64_t lin = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; lin < ntiles; lin += stride) {
+        const int X[3] = {(int)(lin % g.ntl[0]), (int)((lin / g.ntl[0]) % g.ntl[1]),
+                          (int)(lin / ((int64_t)g.ntl[0] * g.ntl[1]))};
+        int f[3] = {0, 0, 0};
+        int64_t r = 0;
+        const int top = max(max(g.mb[0], g.mb[1]), g.mb[2]);
+        for (int k = 0; k < top; ++k) {
+            for (int dp = 0; dp < 3; ++dp) {
+                if (k >= g.mb[dp]) continue;
+                if ((X[dp] >> k) & 1) {
+                    int64_t cnt = 1;
+#pragma unroll
+                    for (int d = 0; d < 3; ++d) {
+                        const int lo = d == dp ? (X[d] >> (k + 1)) << (k + 1) : (X[d] >> f[d]) << f[d];
+                        cnt *= (int64_t)min(max(g.ntl[d] - lo, 0), 1 << f[d]);
+                    }
+                    r += cnt;
+                }
+                ++f[dp];
+            }
+        }
+        tile_of_rank[r] = (int)lin;
+        rank_of_tile[lin] = (int)r;
+    }
 }
 
 // ---------------------------------------------------------------- binning
@@ -188,25 +202,33 @@ __device__ __forceinline__ void small_sort(int* a, int lo, int hi)
     }
 }
 
-// One thread per bin: stable (by atom id) order inside the bin, then the SoA cell list.
-// Bins with more than kBinSortMax atoms keep the atomic arrival order (edge set and
-// counts are unaffected; only the order of edges within a target can then vary).
-__global__ void finish_bins_kernel(int64_t nbins, const int* __restrict__ bstart,
-                                   int* __restrict__ sid, const float4* __restrict__ rec,
-                                   float4* __restrict__ spos, uint32_t* __restrict__ sflr,
+// One thread per cell-list entry j (in arrival order inside its bin, from scatter_atoms):
+// the entry's place in its bin ordered by atom id (the number of smaller ids in the bin),
+// then the SoA cell list.  Bins with more than kBinSortMax atoms keep the atomic arrival
+// order (edge set and counts are unaffected; only the order of edges within a target can
+// then vary).
+__global__ void order_atoms_kernel(int64_t n, const uint32_t* __restrict__ key,
+                                   const int* __restrict__ bstart, const int* __restrict__ arr,
+                                   const float4* __restrict__ rec, float4* __restrict__ spos,
+                                   uint32_t* __restrict__ sflr, int* __restrict__ sid,
                                    int* __restrict__ inv)
 {
-    int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (q >= nbins) return;
-    int lo = bstart[q], hi = bstart[q + 1];
-    if (hi - lo > 1 && hi - lo <= kBinSortMax) small_sort(sid, lo, hi);
-    for (int j = lo; j < hi; ++j) {
-        const int i = sid[j];
-        const float4 r = rec[i];
-        spos[j] = make_float4(r.x, r.y, r.z, __int_as_float(i));
-        sflr[j] = __float_as_uint(r.w);
-        if (inv) inv[i] = j;
+    const int64_t j = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (j >= n) return;
+    const int i = arr[j];
+    const uint32_t b = key[i];
+    const int lo = bstart[b], hi = bstart[b + 1];
+    int d = (int)j;
+    if (hi - lo > 1 && hi - lo <= kBinSortMax) {
+        int below = 0;
+        for (int m = lo; m < hi; ++m) below += arr[m] < i;
+        d = lo + below;
     }
+    const float4 r = rec[i];
+    spos[d] = make_float4(r.x, r.y, r.z, __int_as_float(i));
+    sflr[d] = __float_as_uint(r.w);
+    sid[d] = i;
+    if (inv) inv[i] = d;
 }
 
 // ---------------------------------------------------------------- explicit targets
@@ -1412,17 +1434,12 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
                  int64_t* totals, hipStream_t s)
 {
     GridArgs g = grid_args(p);
-    // 1. Morton rank of the tiles
-    int* cflag = at<int>(ws, p.o_cflag);
-    int* cpos = at<int>(ws, p.o_cpos);
-    hipLaunchKernelGGL(tile_flags_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes, cflag);
-    excl_scan<int, int>(cflag, p.ncodes, cpos, at<int>(ws, p.o_part), s);
-    hipLaunchKernelGGL(tile_fill_kernel, dim3(nblocks(p.ncodes)), dim3(256), 0, s, g, p.ncodes,
-                       cflag, cpos, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot));
-    // 2-5. counting sort of the atoms into SFC-ordered bins
+    // 1. Morton rank of the tiles (and cleared bin counts)
     int* bcnt = at<int>(ws, p.o_bcnt);
     int* bstart = at<int>(ws, p.o_bstart);
-    hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, bcnt, p.nbins);
+    hipLaunchKernelGGL(tile_rank_kernel, dim3((unsigned)std::min<int64_t>(nblocks(p.nbins), 2048)), dim3(256),
+                       0, s, g, p.ntiles, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot), bcnt, p.nbins);
+    // 2-5. counting sort of the atoms into SFC-ordered bins
     hipLaunchKernelGGL(bin_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, g, pos, p.f64, p.n,
                        (const int*)at<int>(ws, p.o_rot), at<uint32_t>(ws, p.o_key),
                        at<uint32_t>(ws, p.o_rank), bcnt, at<float4>(ws, p.o_rec), totals);
@@ -1430,10 +1447,11 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
     hipLaunchKernelGGL(scatter_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, p.n,
                        (const uint32_t*)at<uint32_t>(ws, p.o_key),
                        (const uint32_t*)at<uint32_t>(ws, p.o_rank), (const int*)bstart,
-                       at<int>(ws, p.o_sid));
-    hipLaunchKernelGGL(finish_bins_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, p.nbins,
-                       (const int*)bstart, at<int>(ws, p.o_sid), (const float4*)at<float4>(ws, p.o_rec),
-                       at<float4>(ws, p.o_spos), at<uint32_t>(ws, p.o_sflr),
+                       at<int>(ws, p.o_arr));
+    hipLaunchKernelGGL(order_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, p.n,
+                       (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)bstart,
+                       (const int*)at<int>(ws, p.o_arr), (const float4*)at<float4>(ws, p.o_rec),
+                       at<float4>(ws, p.o_spos), at<uint32_t>(ws, p.o_sflr), at<int>(ws, p.o_sid),
                        p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr);
     if (p.subset) {
         int* tbcnt = at<int>(ws, p.o_tbcnt);

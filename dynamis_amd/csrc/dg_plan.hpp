@@ -40,7 +40,7 @@ struct Plan {
     float hi = 0, lo_in = 0, tiny = 0;
     // workspace layout (byte offsets)
     size_t o_key, o_rank, o_rec, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
-    size_t o_cflag, o_cpos, o_tor, o_rot;
+    size_t o_arr, o_tor, o_rot;  // o_arr: cell-list ids in arrival order (before the in-bin sort)
     size_t o_tkey, o_trank, o_tbcnt, o_tbstart, o_tslot, o_tsidx, o_tcaller;
     size_t o_cnt, o_ttot, o_tfix, o_tbase, o_part, o_tot, o_slot;
     int K = 0;              // neighbour slot entries per target
@@ -193,7 +193,7 @@ inline void plan_layout(Plan& p)
     size_t o = 0;
     auto take = [&](size_t bytes) { size_t r = o; o = align_up(o + (bytes ? bytes : 1)); return r; };
     const size_t n = (size_t)p.n, nt = (size_t)p.nt, nbins = (size_t)p.nbins;
-    const size_t nc = (size_t)p.ncodes, ntl = (size_t)p.ntiles;
+    const size_t ntl = (size_t)p.ntiles;
     p.o_tot = take(8 * 8);
     p.o_key = take(4 * n);
     p.o_rank = take(4 * n);
@@ -204,8 +204,7 @@ inline void plan_layout(Plan& p)
     p.o_spos = take(16 * n);
     p.o_sflr = take(4 * n);
     p.o_inv = take(p.subset ? 4 * n : 0);
-    p.o_cflag = take(4 * nc);
-    p.o_cpos = take(4 * (nc + 1));
+    p.o_arr = take(4 * n);
     p.o_tor = take(4 * ntl);
     p.o_rot = take(4 * ntl);
     p.o_tkey = take(p.subset ? 4 * nt : 0);
@@ -221,7 +220,7 @@ inline void plan_layout(Plan& p)
     p.o_tfix = take(4 * ntl);
     p.o_tbase = take(8 * (std::max(ntl, nt) + 1));
     // scan partials: one int64 per 2048-item block of the largest scan
-    size_t big = std::max(std::max(nbins + 1, nc + 1), std::max(ntl, nt) + 1);
+    size_t big = std::max(nbins + 1, std::max(ntl, nt) + 1);
     p.o_part = take(8 * (big / 2048 + 2));
     p.ws_bytes = o;
 }
