@@ -166,7 +166,7 @@ __global__ void bin_atoms_kernel(GridArgs g, const void* __restrict__ pos, int f
     if (st) atomicOr((unsigned long long*)&totals[1], (unsigned long long)st);
     uint32_t k = bin_key(g, b, rank_of_tile);
     key[i] = k;
-    rank[i] = (uint32_t)atomicAdd(&bcnt[k], 1);
+    if (bcnt) rank[i] = (uint32_t)atomicAdd(&bcnt[k], 1);
     // position relative to the bin origin: (s - b/nb) . C
     double o[3];
 #pragma unroll
@@ -229,6 +229,165 @@ __global__ void order_atoms_kernel(int64_t n, const uint32_t* __restrict__ key,
     sflr[d] = __float_as_uint(r.w);
     sid[d] = i;
     if (inv) inv[i] = d;
+}
+
+// ---------------------------------------------------------------- tile-level counting sort
+// Without per-atom device atomics (about 25 G/s on this part, the dominant cost of a
+// per-bin counting sort): kSortChunks workgroups each histogram the tiles of one chunk of
+// atoms in LDS and reserve their share of every tile with one device atomic per tile;
+// the same chunks then place their atoms into tile buckets; one workgroup per tile then
+// orders its bucket by (bin, atom id) in LDS and writes the bin starts and the cell list.
+
+// Chunk c of the atoms: [c n / G, (c + 1) n / G).
+__device__ __forceinline__ void sort_chunk(int64_t n, int64_t* lo, int64_t* hi)
+{
+    *lo = n * blockIdx.x / gridDim.x;
+    *hi = n * (blockIdx.x + 1) / gridDim.x;
+}
+
+__global__ __launch_bounds__(1024) void tile_hist_kernel(int64_t n, int tb, int64_t ntiles,
+                                                         const uint32_t* __restrict__ key,
+                                                         int* __restrict__ tcnt, int* __restrict__ wgb)
+{
+    extern __shared__ int h[];
+    for (int64_t r = threadIdx.x; r < ntiles; r += blockDim.x) h[r] = 0;
+    __syncthreads();
+    int64_t lo, hi;
+    sort_chunk(n, &lo, &hi);
+    for (int64_t i = lo + threadIdx.x; i < hi; i += blockDim.x) atomicAdd(&h[key[i] / (uint32_t)tb], 1);
+    __syncthreads();
+    for (int64_t r = threadIdx.x; r < ntiles; r += blockDim.x) {
+        const int c = h[r];
+        wgb[blockIdx.x * ntiles + r] = c ? atomicAdd(&tcnt[r], c) : 0;
+    }
+}
+
+// Places every atom of the chunk in its tile's bucket as (atom id, bin inside the tile);
+// the atoms are read in order, the scattered side is the 8-byte stores.
+__global__ __launch_bounds__(1024) void tile_scatter_kernel(int64_t n, int tb, int64_t ntiles,
+                                                            const uint32_t* __restrict__ key,
+                                                            const int* __restrict__ tstart,
+                                                            const int* __restrict__ wgb,
+                                                            uint64_t* __restrict__ bucket)
+{
+    extern __shared__ int h[];  // this chunk's next place in every tile's bucket
+    for (int64_t r = threadIdx.x; r < ntiles; r += blockDim.x)
+        h[r] = tstart[r] + wgb[blockIdx.x * ntiles + r];
+    __syncthreads();
+    int64_t lo, hi;
+    sort_chunk(n, &lo, &hi);
+    // four atoms per thread and step, their loads issued together
+    for (int64_t i0 = lo + threadIdx.x; i0 < hi; i0 += 4 * (int64_t)blockDim.x) {
+        uint32_t k[4];
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = i0 + (int64_t)u * blockDim.x;
+            k[u] = i < hi ? key[i] : 0u;
+        }
+#pragma unroll
+        for (int u = 0; u < 4; ++u) {
+            const int64_t i = i0 + (int64_t)u * blockDim.x;
+            if (i < hi) {
+                const uint32_t r = k[u] / (uint32_t)tb;
+                const int d = atomicAdd(&h[r], 1);
+                bucket[d] = (uint64_t)(uint32_t)i | ((uint64_t)(k[u] - r * (uint32_t)tb) << 32);
+            }
+        }
+    }
+}
+
+constexpr int kTileSortCap = 2048;  // bucket entries ordered in LDS (larger: arrival order in bins)
+constexpr int kTileSortPer = kTileSortCap / 256;
+struct TileSortLds {
+    int id[kTileSortCap];
+    int lb[kTileSortCap];
+    int by[kTileSortCap];  // ids grouped by bin
+    int cnt[kTileMax * kTileMax * kTileMax];
+    int st[kTileMax * kTileMax * kTileMax + 1];
+    int w32[4];
+};
+
+// One workgroup per tile: orders its bucket by (bin, atom id), writes the tile's bin starts
+// and its part of the cell list.  Each entry's record is gathered into registers as soon as
+// its id is known, so the gathers overlap the ordering in LDS.
+__global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64_t ntiles,
+                                                        const int* __restrict__ tstart,
+                                                        const uint64_t* __restrict__ bucket,
+                                                        const float4* __restrict__ rec,
+                                                        int* __restrict__ bstart,
+                                                        float4* __restrict__ spos,
+                                                        uint32_t* __restrict__ sflr,
+                                                        int* __restrict__ sid, int* __restrict__ inv)
+{
+    __shared__ TileSortLds S;
+    const int64_t r = blockIdx.x;
+    const int base = tstart[r], m = tstart[r + 1] - base;
+    const bool fits = m <= kTileSortCap;
+    for (int l = threadIdx.x; l < tb; l += 256) S.cnt[l] = 0;
+    __syncthreads();
+    float4 q[kTileSortPer];
+    int qi[kTileSortPer], ql[kTileSortPer];
+#pragma unroll
+    for (int u = 0; u < kTileSortPer; ++u) {
+        const int e = threadIdx.x + 256 * u;
+        qi[u] = -1;
+        if (fits && e < m) {
+            const uint64_t w = bucket[base + e];
+            qi[u] = (int)(uint32_t)w;
+            ql[u] = (int)(w >> 32);
+            q[u] = rec[qi[u]];
+            S.id[e] = qi[u];
+            S.lb[e] = ql[u];
+            atomicAdd(&S.cnt[ql[u]], 1);
+        }
+    }
+    if (!fits)
+        for (int e = threadIdx.x; e < m; e += 256) atomicAdd(&S.cnt[(int)(bucket[base + e] >> 32)], 1);
+    __syncthreads();
+    // bin starts inside the bucket (tb <= 216: one pass of a 256-thread scan)
+    {
+        const int c = threadIdx.x < tb ? S.cnt[threadIdx.x] : 0;
+        int tot;
+        const int ex = block_excl_scan<int, 256>(c, S.w32, &tot);
+        if (threadIdx.x < tb) {
+            S.st[threadIdx.x] = ex;
+            S.cnt[threadIdx.x] = ex;  // placement cursors
+            bstart[r * tb + threadIdx.x] = base + ex;
+        }
+        if (threadIdx.x == 0) {
+            S.st[tb] = tot;
+            if (r == ntiles - 1) bstart[ntiles * tb] = (int)n;
+        }
+    }
+    __syncthreads();
+    auto emit = [&](int d, int i, float4 v) {
+        spos[d] = make_float4(v.x, v.y, v.z, __int_as_float(i));
+        sflr[d] = __float_as_uint(v.w);
+        sid[d] = i;
+        if (inv) inv[i] = d;
+    };
+    if (!fits) {
+        // a very dense tile: bins in arrival order, records gathered from rec
+        for (int e = threadIdx.x; e < m; e += 256) {
+            const uint64_t w = bucket[base + e];
+            const int i = (int)(uint32_t)w;
+            emit(base + atomicAdd(&S.cnt[(int)(w >> 32)], 1), i, rec[i]);
+        }
+        return;
+    }
+#pragma unroll
+    for (int u = 0; u < kTileSortPer; ++u)
+        if (qi[u] >= 0) S.by[atomicAdd(&S.cnt[ql[u]], 1)] = qi[u];
+    __syncthreads();
+    // each entry's place in its bin: the number of smaller ids there
+#pragma unroll
+    for (int u = 0; u < kTileSortPer; ++u) {
+        if (qi[u] < 0) continue;
+        const int i = qi[u], l = ql[u];
+        int below = 0;
+        for (int k = S.st[l]; k < S.st[l + 1]; ++k) below += S.by[k] < i;
+        emit(base + S.st[l] + below, i, q[u]);
+    }
 }
 
 // ---------------------------------------------------------------- explicit targets
@@ -1434,12 +1593,39 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
                  int64_t* totals, hipStream_t s)
 {
     GridArgs g = grid_args(p);
-    // 1. Morton rank of the tiles (and cleared bin counts)
     int* bcnt = at<int>(ws, p.o_bcnt);
     int* bstart = at<int>(ws, p.o_bstart);
+    if (p.ntiles <= kSortTilesMax) {
+        // 1. Morton rank of the tiles (and cleared tile counts)
+        int* tcnt = at<int>(ws, p.o_tcnt);
+        int* tstart = at<int>(ws, p.o_tstart);
+        int* wgb = at<int>(ws, p.o_wgb);
+        hipLaunchKernelGGL(tile_rank_kernel, dim3((unsigned)std::min<int64_t>(nblocks(p.ntiles), 2048)),
+                           dim3(256), 0, s, g, p.ntiles, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot), tcnt,
+                           p.ntiles);
+        // 2. wrap, bin key and cell-list record of every atom
+        hipLaunchKernelGGL(bin_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, g, pos, p.f64, p.n,
+                           (const int*)at<int>(ws, p.o_rot), at<uint32_t>(ws, p.o_key),
+                           (uint32_t*)nullptr, (int*)nullptr, at<float4>(ws, p.o_rec), totals);
+        // 3-5. tile buckets, then each tile's bins in LDS
+        const unsigned nch = (unsigned)std::max<int64_t>(1, std::min<int64_t>(kSortChunks, (p.n + 4095) / 4096));
+        const size_t hl = 4 * (size_t)p.ntiles;
+        hipLaunchKernelGGL(tile_hist_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
+                           (const uint32_t*)at<uint32_t>(ws, p.o_key), tcnt, wgb);
+        excl_scan<int, int>(tcnt, p.ntiles, tstart, at<int>(ws, p.o_part), s);
+        hipLaunchKernelGGL(tile_scatter_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
+                           (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)tstart,
+                           (const int*)wgb, at<uint64_t>(ws, p.o_arr));
+        hipLaunchKernelGGL(tile_sort_kernel, dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n, p.tb,
+                           p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_arr),
+                           (const float4*)at<float4>(ws, p.o_rec), bstart, at<float4>(ws, p.o_spos),
+                           at<uint32_t>(ws, p.o_sflr), at<int>(ws, p.o_sid),
+                           p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr);
+    } else {
+    // 1. Morton rank of the tiles (and cleared bin counts)
     hipLaunchKernelGGL(tile_rank_kernel, dim3((unsigned)std::min<int64_t>(nblocks(p.nbins), 2048)), dim3(256),
                        0, s, g, p.ntiles, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot), bcnt, p.nbins);
-    // 2-5. counting sort of the atoms into SFC-ordered bins
+    // 2-5. counting sort of the atoms into SFC-ordered bins (per-bin device atomics)
     hipLaunchKernelGGL(bin_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, g, pos, p.f64, p.n,
                        (const int*)at<int>(ws, p.o_rot), at<uint32_t>(ws, p.o_key),
                        at<uint32_t>(ws, p.o_rank), bcnt, at<float4>(ws, p.o_rec), totals);
@@ -1453,6 +1639,7 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
                        (const int*)at<int>(ws, p.o_arr), (const float4*)at<float4>(ws, p.o_rec),
                        at<float4>(ws, p.o_spos), at<uint32_t>(ws, p.o_sflr), at<int>(ws, p.o_sid),
                        p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr);
+    }
     if (p.subset) {
         int* tbcnt = at<int>(ws, p.o_tbcnt);
         int* tbstart = at<int>(ws, p.o_tbstart);

@@ -18,6 +18,8 @@
 namespace dg {
 
 constexpr int kBlock = 256;      // threads per search workgroup (4 x wave64)
+constexpr int kSortChunks = 64;      // atom chunks of the tile-level counting sort
+constexpr int kSortTilesMax = 16000;  // tiles it handles (an LDS histogram of ints, < 64 KiB)
 constexpr int kMaxRegion = 768;  // region bins staged per tile
 constexpr int kTileTargets = 235; // aim: targets per tile <= this (a 256-lane workgroup)
 constexpr int kTileMax = 6;       // bins per tile along one axis
@@ -41,6 +43,7 @@ struct Plan {
     // workspace layout (byte offsets)
     size_t o_key, o_rank, o_rec, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
     size_t o_arr, o_tor, o_rot;  // o_arr: cell-list ids in arrival order (before the in-bin sort)
+    size_t o_tcnt, o_tstart, o_wgb;  // tile-level counting sort: tile totals, starts, chunk bases
     size_t o_tkey, o_trank, o_tbcnt, o_tbstart, o_tslot, o_tsidx, o_tcaller;
     size_t o_cnt, o_ttot, o_tfix, o_tbase, o_part, o_tot, o_slot;
     int K = 0;              // neighbour slot entries per target
@@ -204,7 +207,10 @@ inline void plan_layout(Plan& p)
     p.o_spos = take(16 * n);
     p.o_sflr = take(4 * n);
     p.o_inv = take(p.subset ? 4 * n : 0);
-    p.o_arr = take(4 * n);
+    p.o_arr = take(8 * n);
+    p.o_tcnt = take(4 * ntl);
+    p.o_tstart = take(4 * (ntl + 1));
+    p.o_wgb = take(4 * (size_t)kSortChunks * ntl);
     p.o_tor = take(4 * ntl);
     p.o_rot = take(4 * ntl);
     p.o_tkey = take(p.subset ? 4 * nt : 0);
