@@ -517,6 +517,16 @@ constexpr int kQBytes = (int)sizeof(float4) * (kCap + 1);
 static_assert(sizeof(ExpandStage) <= (size_t)kQBytes, "expansion view exceeds the region buffer");
 
 constexpr int kRing = 16;  // slot entries a lane stages in LDS (two groups of 8)
+
+// Byte address of ring entry k2 / 2 (mod 16) of the lane whose ring starts at byte lane_off
+// (a multiple of 32): lane_off | (k2 & 30) in one VALU op (the compiler emits an and and an
+// add for it).
+__device__ __forceinline__ uint32_t ring_at(int k2, uint32_t lane_off)
+{
+    uint32_t r;
+    asm("v_and_or_b32 %0, %1, 30, %2" : "=v"(r) : "v"(k2), "v"(lane_off));
+    return r;
+}
 struct SearchLds {
     __align__(16) unsigned char qbuf[kQBytes];
     int tbs[kTileMax * kTileMax * kTileMax + 1];  // bin starts of the tile
@@ -784,7 +794,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, ExpandLds& sh, 
 #pragma unroll
             for (int u = 0; u < kExpandIlp; ++u) {
                 rok[u] = L.kk[u] < a.K;
-                const int2 en = X.e[rok[u] ? min(L.raw[u], kCap) : kCap];
+                const int2 en = X.e[rok[u] ? min(L.raw[u] >> 4, kCap) : kCap];
                 const uint32_t ft = B.tf[L.tt[u]];
                 rs[u] = en.x;
                 rd[u] = B.tid[L.tt[u]];
@@ -1099,7 +1109,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
 
         // Sweep this lane's target over the resident chunk c, in the fixed order (dz, dy,
         // x, atom) -- ascending region index; on_cand(v, edge, k) receives every candidate's
-        // chunk-local region index, whether it is an edge, and twice the running neighbour
+        // byte offset in the chunk (16 x its chunk-local region index), whether it is an
+        // edge, and twice the running neighbour
         // number, k2 = 2 k (k: the edge's number when it is one); on_step(k2) follows every
         // step of two candidates, on_row(k2) every row.
         //
@@ -1139,29 +1150,35 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             va = max(sh.rp[rb + xlo], c0) - c0;
             vb = min(sh.rp[rb + xhi + 1], c1) - c0;
             if (va >= vb) va = vb = 0;
+            va <<= 4;  // byte offsets of the 16-byte entries
+            vb <<= 4;
         };
         auto sweep = [&](int c, auto&& on_cand, auto&& on_step, auto&& on_row) {
             const int c0 = c * kCap;
             const int c1 = min(total, c0 + kCap);
-            const int vs = v_self - c0;
+            const int vs = (v_self - c0) << 4;
             const int nrows = nrz * nry;
-            // [v, e): this lane's unswept part of its current row (row cur); [pv, pe): its
-            // next row.  A lane moves on to its next row the step it finishes its current
-            // one, so when the wave leaves row ri every lane is on its row ri + 1.
-            int v, e, pv = 0, pe = 0, cur = 0;
+            const char* const qb = (const char*)shq;
+            // Candidates are addressed by the byte offset of their 16-byte entry in shq.
+            // [v, e): this lane's unswept part of its current row; [pv, pe): its next row,
+            // pv == pe once the lane has moved on to it (an empty or missing next row is
+            // [16, 0) until then).  A lane moves on to its next row the step it finishes its
+            // current one, so when the wave leaves row ri every lane is on its row ri + 1.
+            int v, e, pv, pe;
             row_range(0, c0, c1, v, e);
             if (!active) v = e = 0;
             for (int ri = 0; ri < nrows; ++ri) {
-                pv = pe = 0;  // (the last row has no next row)
+                pv = 0; pe = 0;
                 if (ri + 1 < nrows && active) row_range(ri + 1, c0, c1, pv, pe);
-                if (v >= e) { v = pv; e = pe; cur = ri + 1; }  // nothing left of row ri
+                if (pv == pe) { pv = 16; pe = 0; }
+                if (v >= e) { v = pv; e = pe; pv = pe; }  // nothing left of row ri
                 // two candidates per step, both loads issued first (the second may be one
                 // past the range -- at most the sentinel -- and is then masked); the edge
                 // test is branch-free, the rare exact test sits behind a scalar mask test,
                 // and on_cand sees every candidate in order
-                if (__builtin_amdgcn_ballot_w64(cur == ri) != 0ull) do {
-                    const float4 q0 = shq[v], q1 = shq[v + 1];
-                    const bool in0 = v < e, in1 = v + 1 < e;
+                if (__builtin_amdgcn_ballot_w64(pv != pe) != 0ull) do {
+                    const float4 q0 = *(const float4*)(qb + v), q1 = *(const float4*)(qb + v + 16);
+                    const bool in0 = v < e, in1 = v + 16 < e;
                     float dx = q0.x - t0, dyv = q0.y - t1, dzv = q0.z - t2;
                     const float d20 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
                     dx = q1.x - t0; dyv = q1.y - t1; dzv = q1.z - t2;
@@ -1169,7 +1186,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                     bool e0 = in0 & (d20 < a.lo_in) & (d20 > a.tiny);
                     bool e1 = in1 & (d21 < a.lo_in) & (d21 > a.tiny);
                     const bool b0 = in0 & !e0 & (d20 <= a.hi) & (v != vs);
-                    const bool b1 = in1 & !e1 & (d21 <= a.hi) & (v + 1 != vs);
+                    const bool b1 = in1 & !e1 & (d21 <= a.hi) & (v + 16 != vs);
                     if (__builtin_expect(b0 | b1, 0)) {  // divergent: the mask test is scalar
                         if (b0)
                             e0 = exact_edge(a, __float_as_int(q0.w), my_id, (double)q0.x - t0,
@@ -1181,17 +1198,18 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                     // (a candidate past the range is no edge: k does not advance)
                     on_cand(v, e0, found2);
                     found2 += e0 ? 2 : 0;
-                    on_cand(v + 1, e1, found2);
+                    on_cand(v + 16, e1, found2);
                     found2 += e1 ? 2 : 0;
                     on_step(found2);
                     // range done: from row ri on to the next row, from that one to rest (at
                     // v = e: masked loads of entries e and e + 1, inside LDS)
-                    const int nv = v + 2;
-                    const bool fin = nv >= e, sw = fin & (cur == ri);
-                    v = fin ? (sw ? pv : e) : nv;
-                    e = sw ? pe : e;
-                    cur = sw ? ri + 1 : cur;
-                } while (__builtin_amdgcn_ballot_w64(cur == ri) != 0ull);
+                    // (a lane already on its next row that finishes it takes [pe, pe): empty)
+                    const int nv = v + 32;
+                    const bool fin = nv >= e;
+                    v = fin ? pv : nv;
+                    e = fin ? pe : e;
+                    pv = fin ? pe : pv;
+                } while (__builtin_amdgcn_ballot_w64(pv != pe) != 0ull);
                 on_row(found2);
             }
         };
@@ -1203,17 +1221,23 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             // written for every candidate (an edge keeps it: k advances), and full groups
             // of 8 go out to the slot at the end of each row -- or within the row, before
             // the ring could wrap onto a group not yet stored.
-            uint16_t* lb = sh.lb[threadIdx.x];
-            char* const lbb = (char*)lb;
+            // this lane's ring: byte lane_off of sh.lb (its low five bits clear, so an entry's
+            // byte address is lane_off | (k2 & 30), one bitwise VALU)
+            static_assert(2 * kRing == 32, "ring of 16 two-byte entries per lane");
+            char* const lb0 = (char*)&sh.lb[0][0];
+            const uint32_t lane_off = threadIdx.x << 5;
+            char* const lbb = lb0 + lane_off;
             const bool slots = one_chunk && a.slot != nullptr;
             char* const slotb = (char*)a.slot;
             const uint32_t gstep = 16u * (uint32_t)a.nslot;  // bytes between a target's groups
             uint32_t goff = 16u * (uint32_t)j;                // byte offset of group kf2 / 16
             int kf2 = 0;                                      // 2 x entries stored (or skipped)
+            int klim = 2 * kRing - 4;                         // kf2 + 28: the in-row flush mark
             const int K2 = 2 * a.K;
             auto store_group = [&]() {  // the group starting at entry kf2 / 2
                 if (kf2 + 16 <= K2) *(uint4*)(slotb + goff) = *(const uint4*)(lbb + (kf2 & 16));
                 kf2 += 16;
+                klim += 16;
                 goff += gstep;
             };
             auto flush = [&](int k2) {  // every full group below entry k2 / 2
@@ -1223,10 +1247,12 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 ensure_chunk(c);
                 if (!active) continue;
                 if (slots) {
-                    sweep(c, [&](int v, bool, int k2) { *(uint16_t*)(lbb + (k2 & (2 * kRing - 2))) = (uint16_t)v; },
+                    sweep(c, [&](int v, bool, int k2) {
+                              *(uint16_t*)(lb0 + ring_at(k2, lane_off)) = (uint16_t)v;
+                          },
                           [&](int k2) {
                               // k2 - kf2 <= 32 here: at most two groups to store
-                              if (k2 - kf2 > 2 * kRing - 4) {
+                              if (k2 > klim) {
                                   store_group();
                                   if (k2 - kf2 >= 16) store_group();
                               }
@@ -1263,8 +1289,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 ensure_chunk(0);
                 if (over) {
                     const int64_t base = ebase + ex;
-                    sweep(0, [&](int v, bool e, int k2) {
-                        const int k = k2 >> 1;
+                    sweep(0, [&](int vb, bool e, int k2) {
+                        const int k = k2 >> 1, v = vb >> 4;
                         if (e && k >= a.K && k < mycnt) {
                             const uint32_t Tp = sh.T[v];
                             emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
@@ -1279,8 +1305,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             for (int c = 0; c < nchunks; ++c) {
                 ensure_chunk(c);
                 if (!active) continue;
-                sweep(c, [&](int v, bool e, int k2) {
-                    const int k = k2 >> 1;
+                sweep(c, [&](int vb, bool e, int k2) {
+                    const int k = k2 >> 1, v = vb >> 4;
                     if (e && k < mycnt) {
                         const uint32_t Tp = sh.T[v];
                         emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
