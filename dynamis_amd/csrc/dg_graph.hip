@@ -446,7 +446,8 @@ struct SearchArgs {
     int nb[3], P[3], T[3], ntl[3], R[3], pbc[3];
     int tb, nregion;
     int64_t ntiles;
-    float hi, lo_in, tiny;
+    float toff, hi_off;  // d2' = d2 - toff: edge iff bits(d2') < lo_bits, band iff d2' <= hi_off
+    uint32_t lo_bits;
     const float4* spos;
     const uint32_t* sflr;
     const int* sid;    // atom id of every cell-list entry
@@ -1179,14 +1180,16 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 if (__builtin_amdgcn_ballot_w64(pv != pe) != 0ull) do {
                     const float4 q0 = *(const float4*)(qb + v), q1 = *(const float4*)(qb + v + 16);
                     const bool in0 = v < e, in1 = v + 16 < e;
+                    // d2 - toff with the offset in the innermost fma; edge iff its bits are
+                    // below lo_bits (0 <= d2' < lo_off), band iff d2' <= hi_off
                     float dx = q0.x - t0, dyv = q0.y - t1, dzv = q0.z - t2;
-                    const float d20 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
+                    const float d20 = fmaf(dzv, dzv, fmaf(dyv, dyv, fmaf(dx, dx, -a.toff)));
                     dx = q1.x - t0; dyv = q1.y - t1; dzv = q1.z - t2;
-                    const float d21 = fmaf(dzv, dzv, fmaf(dyv, dyv, dx * dx));
-                    bool e0 = in0 & (d20 < a.lo_in) & (d20 > a.tiny);
-                    bool e1 = in1 & (d21 < a.lo_in) & (d21 > a.tiny);
-                    const bool b0 = in0 & !e0 & (d20 <= a.hi) & (v != vs);
-                    const bool b1 = in1 & !e1 & (d21 <= a.hi) & (v + 16 != vs);
+                    const float d21 = fmaf(dzv, dzv, fmaf(dyv, dyv, fmaf(dx, dx, -a.toff)));
+                    bool e0 = in0 & (__float_as_uint(d20) < a.lo_bits);
+                    bool e1 = in1 & (__float_as_uint(d21) < a.lo_bits);
+                    const bool b0 = in0 & !e0 & (d20 <= a.hi_off) & (v != vs);
+                    const bool b1 = in1 & !e1 & (d21 <= a.hi_off) & (v + 16 != vs);
                     if (__builtin_expect(b0 | b1, 0)) {  // divergent: the mask test is scalar
                         if (b0)
                             e0 = exact_edge(a, __float_as_int(q0.w), my_id, (double)q0.x - t0,
@@ -1569,7 +1572,7 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.tb = p.tb;
     a.nregion = p.nregion;
     a.ntiles = p.ntiles;
-    a.hi = p.hi; a.lo_in = p.lo_in; a.tiny = p.tiny;
+    a.toff = p.toff; a.hi_off = p.hi_off; a.lo_bits = p.lo_bits;
     a.spos = at<float4>(ws, p.o_spos);
     a.sflr = at<uint32_t>(ws, p.o_sflr);
     a.sid = at<int>(ws, p.o_sid);

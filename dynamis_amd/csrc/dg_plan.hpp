@@ -40,6 +40,8 @@ struct Plan {
     int brute = 0;          // region too large: all-pairs path
     int kimg[3];            // brute path: |S_d| range on periodic axes
     float hi = 0, lo_in = 0, tiny = 0;
+    float toff = 0, hi_off = 0;  // the same bounds on d2 - toff (see plan_grid)
+    uint32_t lo_bits = 0;        // bits of the fp32 bound lo_off on d2 - toff
     // workspace layout (byte offsets)
     size_t o_key, o_rank, o_rec, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
     size_t o_arr, o_tor, o_rot;  // o_arr: cell-list ids in arrival order (before the in-bin sort)
@@ -179,6 +181,26 @@ inline void plan_grid(Plan& p)
     p.lo_in = lo > 0 ? nextafterf((float)lo, 0.0f) : 0.0f;
     double t = sqrt(kSelfThr) + 2.0 * sqrt(3.0) * delta;
     p.tiny = nextafterf((float)(t * t * (1.0 + 1e-3)), INFINITY);
+    // The kernels evaluate d2' = fl(dz² + (dy² + (dx² - toff))), the offset folded into the
+    // innermost fma: three roundings as for d2, so d2' is within the same band of the
+    // exact d2 - toff.  A candidate is an edge without the exact test iff 0 <= d2' <
+    // lo_off: one unsigned compare of the bits (a negative d2' has its sign bit set).
+    // d2' >= 0 gives d2 >= toff (1 - 6u) > tiny's square-root bound, as d2 > tiny did; the
+    // fast upper end and the band end move down by toff, rounded inwards (lo) and
+    // outwards (hi), one more fp32 step each.
+    p.toff = nextafterf(p.tiny, INFINITY);
+    const double lo2 = (double)p.lo_in - (double)p.toff;
+    float lo_off = 0.0f;
+    if (lo2 > 0) {
+        lo_off = (float)lo2;
+        if ((double)lo_off > lo2) lo_off = nextafterf(lo_off, 0.0f);
+        lo_off = nextafterf(lo_off, 0.0f);
+    }
+    memcpy(&p.lo_bits, &lo_off, 4);
+    const double hi2 = (double)p.hi - (double)p.toff;
+    p.hi_off = (float)hi2;
+    if ((double)p.hi_off < hi2) p.hi_off = nextafterf(p.hi_off, INFINITY);
+    p.hi_off = nextafterf(p.hi_off, INFINITY);
 
     // Neighbour slot per target: the expected degree at the mean density with ample
     // headroom (targets past it are swept a second time in the write pass).

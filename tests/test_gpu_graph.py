@@ -275,3 +275,30 @@ def test_near_cutoff_pairs(cuda, dtype, shape):
     pos = _near_cutoff_box(cell, 6.0, 1500, 17, dtype)
     _, _, cnt, o = check_parity(pos, cell, (1, 1, 1), 6.0, cuda, name=f"near-cutoff {shape}")
     assert len(o["src"]) > 1500 * 4  # the inside half of every anchor's partners at least
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape", ["cubic", "general"])
+def test_near_coincident_atoms(cuda, dtype, shape):
+    """Distinct atoms at or near the same place: exact duplicates (d2 = 0, never an edge)
+    and partners at distances around 1e-4 A, where the canonical d2 > 1e-8 threshold
+    decides; some anchors sit on periodic faces, so the duplicate is an image."""
+    cell = {"cubic": np.eye(3) * 60.0,
+            "general": np.array([[60.0, 4.0, -3.0], [10.0, 58.0, 3.0], [-5.0, 7.0, 55.0]])}[shape]
+    rng = np.random.default_rng(29)
+    n = 400
+    f = rng.uniform(0, 1, (n, 3))
+    f[: n // 4, 0] = 0.0  # on a face: partners across it are periodic images
+    anchors = f @ cell
+    dist = np.array([0.0, 0.0, 5e-5, 9e-5, 9.9e-5, 1e-4, 1.01e-4, 1.1e-4, 2e-4, 1e-3])
+    d = rng.normal(size=(n, len(dist), 3))
+    d /= np.linalg.norm(d, axis=-1, keepdims=True)
+    partners = anchors[:, None, :] + d * dist[None, :, None]
+    pos = np.concatenate([anchors, partners.reshape(-1, 3)]).astype(dtype)
+    _, _, _, o = check_parity(pos, cell, (1, 1, 1), 5.0, cuda, name=f"near-coincident {shape}")
+    c = np.asarray(cell, np.float64).astype(dtype).astype(np.float64)
+    _, d2 = oracle.edge_vectors(pos, c, o["src"], o["dst"], o["shift"])
+    # thousands of pairs within 3 % above the threshold (1e-8 rounded to fp32, as the
+    # reference writes it), none at or below it
+    thr = float(np.float32(1e-8))
+    assert np.all(d2 > thr) and np.sum(d2 < 1.03 * thr) > 1000
