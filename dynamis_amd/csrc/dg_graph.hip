@@ -81,9 +81,10 @@ struct GridArgs {
 // Also clears the bin counts (bcnt) for the binning that follows.
 __global__ void tile_rank_kernel(GridArgs g, int64_t ntiles, int* __restrict__ tile_of_rank,
                                  int* __restrict__ rank_of_tile, int* __restrict__ bcnt,
-                                 int64_t nbins)
+                                 int64_t nbins, int64_t* __restrict__ totals)
 {
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    if (blockIdx.x == 0 && threadIdx.x < 8) totals[threadIdx.x] = 0;  // the build's totals and flags
     for (int64_t q = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; q < nbins; q += stride) bcnt[q] = 0;
     for (int64_t lin = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; lin < ntiles; lin += stride) {
         const int X[3] = {(int)(lin % g.ntl[0]), (int)((lin / g.ntl[0]) % g.ntl[1]),
@@ -264,15 +265,35 @@ __global__ __launch_bounds__(1024) void tile_hist_kernel(int64_t n, int tb, int6
 
 // Places every atom of the chunk in its tile's bucket as (atom id, bin inside the tile);
 // the atoms are read in order, the scattered side is the 8-byte stores.
+// Each workgroup scans the tile totals itself (workgroup 0 also stores the tile starts,
+// with tstart[ntiles] = n, for tile_sort_kernel).
 __global__ __launch_bounds__(1024) void tile_scatter_kernel(int64_t n, int tb, int64_t ntiles,
                                                             const uint32_t* __restrict__ key,
-                                                            const int* __restrict__ tstart,
+                                                            const int* __restrict__ tcnt,
+                                                            int* __restrict__ tstart,
                                                             const int* __restrict__ wgb,
                                                             uint64_t* __restrict__ bucket)
 {
     extern __shared__ int h[];  // this chunk's next place in every tile's bucket
-    for (int64_t r = threadIdx.x; r < ntiles; r += blockDim.x)
-        h[r] = tstart[r] + wgb[blockIdx.x * ntiles + r];
+    __shared__ int s_w[1024 / 64];
+    {
+        const int per = (int)((ntiles + 1023) / 1024);
+        const int64_t r0 = (int64_t)threadIdx.x * per;
+        int loc = 0;
+        for (int k = 0; k < per; ++k)
+            if (r0 + k < ntiles) loc += tcnt[r0 + k];
+        int tot;
+        int ex = block_excl_scan<int, 1024>(loc, s_w, &tot);
+        for (int k = 0; k < per; ++k) {
+            const int64_t r = r0 + k;
+            if (r < ntiles) {
+                h[r] = ex + wgb[blockIdx.x * ntiles + r];
+                if (blockIdx.x == 0) tstart[r] = ex;
+                ex += tcnt[r];
+            }
+        }
+        if (blockIdx.x == 0 && threadIdx.x == 0) tstart[ntiles] = tot;
+    }
     __syncthreads();
     int64_t lo, hi;
     sort_chunk(n, &lo, &hi);
@@ -937,7 +958,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, ExpandLds& sh, 
 // every edge and on its order.
 //
 // MODE 0 (count): per-target degree, per-tile total, and -- for tiles whose region fits
-//   in one chunk -- the target's neighbours as 2-byte LDS region indices in its slot of
+//   in one chunk -- the target's neighbours as 2-byte LDS entry byte offsets in its slot of
 //   K entries (written 16 bytes at a time through a per-lane LDS buffer).
 // MODE 1 (fix-up write, only tiles the count pass flagged): targets with more than K
 //   neighbours get their edges k >= K by a second sweep, tiles with a chunked region are
@@ -1631,7 +1652,7 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         int* wgb = at<int>(ws, p.o_wgb);
         hipLaunchKernelGGL(tile_rank_kernel, dim3((unsigned)std::min<int64_t>(nblocks(p.ntiles), 2048)),
                            dim3(256), 0, s, g, p.ntiles, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot), tcnt,
-                           p.ntiles);
+                           p.ntiles, totals);
         // 2. wrap, bin key and cell-list record of every atom
         hipLaunchKernelGGL(bin_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, g, pos, p.f64, p.n,
                            (const int*)at<int>(ws, p.o_rot), at<uint32_t>(ws, p.o_key),
@@ -1641,9 +1662,8 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         const size_t hl = 4 * (size_t)p.ntiles;
         hipLaunchKernelGGL(tile_hist_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
                            (const uint32_t*)at<uint32_t>(ws, p.o_key), tcnt, wgb);
-        excl_scan<int, int>(tcnt, p.ntiles, tstart, at<int>(ws, p.o_part), s);
         hipLaunchKernelGGL(tile_scatter_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
-                           (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)tstart,
+                           (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)tcnt, tstart,
                            (const int*)wgb, at<uint64_t>(ws, p.o_arr));
         hipLaunchKernelGGL(tile_sort_kernel, dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n, p.tb,
                            p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_arr),
@@ -1653,7 +1673,7 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
     } else {
     // 1. Morton rank of the tiles (and cleared bin counts)
     hipLaunchKernelGGL(tile_rank_kernel, dim3((unsigned)std::min<int64_t>(nblocks(p.nbins), 2048)), dim3(256),
-                       0, s, g, p.ntiles, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot), bcnt, p.nbins);
+                       0, s, g, p.ntiles, at<int>(ws, p.o_tor), at<int>(ws, p.o_rot), bcnt, p.nbins, totals);
     // 2-5. counting sort of the atoms into SFC-ordered bins (per-bin device atomics)
     hipLaunchKernelGGL(bin_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, g, pos, p.f64, p.n,
                        (const int*)at<int>(ws, p.o_rot), at<uint32_t>(ws, p.o_key),
@@ -1715,7 +1735,8 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
     if (p.subset && p.nt > 0 && !target_idx) return fail(DG_ERR_INVALID, "target_idx is NULL");
     g_last_error.clear();
     int64_t* totals = at<int64_t>(ws, p.o_tot);
-    hipLaunchKernelGGL(zero_i64_kernel, dim3(1), dim3(64), 0, s, totals, (int64_t)8);
+    if (p.n == 0 || p.nt == 0 || p.brute)  // (else tile_rank_kernel clears them)
+        hipLaunchKernelGGL(zero_i64_kernel, dim3(1), dim3(64), 0, s, totals, (int64_t)8);
     if (p.n == 0 || p.nt == 0) {
         if (counts_out && p.nt > 0)
             hipLaunchKernelGGL(zero_i32_kernel, dim3(nblocks(p.nt)), dim3(256), 0, s, counts_out, p.nt);
