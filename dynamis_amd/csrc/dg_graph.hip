@@ -50,7 +50,8 @@ constexpr int kBinSortMax = 128;
 constexpr int kExpandIlp = 4;  // 64-edge steps per iteration of the expansion (even)
 // search_kernel<1> work of a tile, set by the count pass
 constexpr int kFixOver = 1;     // a target has more than K neighbours
-constexpr int kFixChunked = 2;  // the region does not fit one LDS chunk (or no slots)
+constexpr int kFixChunked = 2;  // the region needs more than two LDS chunks (or no slots)
+constexpr int kFix2 = 4;        // the region needs two LDS chunks (slots hold both)
 
 // Value known to be uniform across the wave, moved to a scalar register.
 __device__ __forceinline__ int rfl(int x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -524,12 +525,15 @@ __device__ __forceinline__ int64_t xcd_tile_rank(int64_t b, int64_t ntiles)
 // The count pass adds the per-lane slot staging (lb) and still fits four workgroups per
 // CU; the fix-up write pass adds the per-entry shift table T.
 constexpr int kStage = 64 * kExpandIlp;  // edges one wave stages per step
-struct ExpandStage {
-    int2 e[kCap + 1];  // per region entry: source atom id, packed (bin shift - floor)
+// CAP: region entries staged (one LDS chunk, or two for the dense tiles of expand2)
+template <int CAP>
+struct ExpandStageT {
+    int2 e[CAP + 1];  // per region entry: source atom id, packed (bin shift - floor)
     int st_src[kBlock / 64][kStage];
     int st_dst[kBlock / 64][kStage];
     uint32_t st_S[kBlock / 64][kStage];
 };
+typedef ExpandStageT<kCap> ExpandStage;
 struct BatchTab {
     int off[kBlock + 1];  // edge offsets of the batch's targets
     int tid[kBlock];
@@ -567,6 +571,17 @@ struct FixLds : SearchLds {
 struct ExpandLds : SearchLds {
     BatchTab bt;
 };
+// The expansion of two-chunk tiles: the same members, a region buffer for 2 kCap entries.
+struct Expand2Lds {
+    __align__(16) unsigned char qbuf[sizeof(ExpandStageT<2 * kCap>)];
+    int tbs[kTileMax * kTileMax * kTileMax + 1];
+    int64_t w64[kBlock / 64];
+    int w32[kBlock / 64];
+    int64_t bc[2];
+    BatchTab bt;
+};
+template <int CAP> struct ExpandLdsOf { typedef ExpandLds type; };
+template <> struct ExpandLdsOf<2 * kCap> { typedef Expand2Lds type; };
 static_assert(sizeof(CountLds) <= 40960, "count pass must fit four workgroups per CU");
 template <int MODE>
 struct LdsOf { typedef CountLds type; };
@@ -696,9 +711,11 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // Stages the tile's region into ExpandStage::e as (source atom id, packed bin shift -
 // floor) pairs -- 8 bytes per entry -- bin by bin from the cell list.  The caller has
 // finished every use of the float4 view of the region buffer.
-__device__ __forceinline__ void stage_pairs(const SearchArgs& a, ExpandLds& sh, const int* g0)
+template <int CAP>
+__device__ __forceinline__ void stage_pairs(const SearchArgs& a, typename ExpandLdsOf<CAP>::type& sh,
+                                            const int* g0)
 {
-    ExpandStage& X = *(ExpandStage*)sh.qbuf;
+    ExpandStageT<CAP>& X = *(ExpandStageT<CAP>*)sh.qbuf;
     {
         int rcnt[kRegPerThread], rst[kRegPerThread];
         const int mysum = region_bins(a, g0, rcnt, rst);
@@ -726,7 +743,7 @@ __device__ __forceinline__ void stage_pairs(const SearchArgs& a, ExpandLds& sh, 
             }
             ex += rcnt[h];
         }
-        if (threadIdx.x == 0) X.e[kCap] = make_int2(0, 0);
+        if (threadIdx.x == 0) X.e[CAP] = make_int2(0, 0);
     }
 
 }
@@ -736,11 +753,11 @@ __device__ __forceinline__ void stage_pairs(const SearchArgs& a, ExpandLds& sh, 
 // targets has its edges split evenly over the waves; a wave walks its range 64 edges at a
 // time, lane e finding its target by a short forward walk from the wave's current target.
 // Edges k >= K are left to search_kernel<1>.  PLAIN: no vector / distance outputs.
-template <bool PLAIN>
-__device__ __forceinline__ void expand_tile(const SearchArgs& a, ExpandLds& sh, int tbeg, int ntg,
-                                            int64_t ebase)
+template <bool PLAIN, int CAP>
+__device__ __forceinline__ void expand_tile(const SearchArgs& a, typename ExpandLdsOf<CAP>::type& sh,
+                                            int tbeg, int ntg, int64_t ebase)
 {
-    ExpandStage& X = *(ExpandStage*)sh.qbuf;
+    ExpandStageT<CAP>& X = *(ExpandStageT<CAP>*)sh.qbuf;
     BatchTab& B = sh.bt;
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
@@ -816,7 +833,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, ExpandLds& sh, 
 #pragma unroll
             for (int u = 0; u < kExpandIlp; ++u) {
                 rok[u] = L.kk[u] < a.K;
-                const int2 en = X.e[rok[u] ? min(L.raw[u] >> 4, kCap) : kCap];
+                const int2 en = X.e[rok[u] ? min(L.raw[u] >> 4, CAP) : CAP];
                 const uint32_t ft = B.tf[L.tt[u]];
                 rs[u] = en.x;
                 rd[u] = B.tid[L.tt[u]];
@@ -1002,7 +1019,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         }
         return out;
     }
-    if (WRITE && a.tfix[ord] == 0) return out;  // the expansion wrote the whole tile
+    if (WRITE && (a.tfix[ord] & (kFixOver | kFixChunked)) == 0) return out;  // written by an expansion
     for (int k = threadIdx.x; k <= a.tb; k += kBlock) sh.tbs[k] = tstart[kb + k];
 
     int64_t ebase = 0;
@@ -1034,7 +1051,9 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
     }
     __syncthreads();
     const int nchunks = (total + kCap - 1) / kCap;
-    const bool one_chunk = nchunks <= 1;
+    // slots hold up to two chunks' entries (2-byte byte offsets in the region); a larger
+    // region is written directly by search_kernel<1>
+    const bool slotted = nchunks <= 2 && a.slot != nullptr;
     int loaded = -1;
 
     // packed (image shift of region bin rb - floor of cell-list entry gidx)
@@ -1251,7 +1270,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             char* const lb0 = (char*)&sh.lb[0][0];
             const uint32_t lane_off = threadIdx.x << 5;
             char* const lbb = lb0 + lane_off;
-            const bool slots = one_chunk && a.slot != nullptr;
+            const bool slots = slotted;
             char* const slotb = (char*)a.slot;
             const uint32_t gstep = 16u * (uint32_t)a.nslot;  // bytes between a target's groups
             uint32_t goff = 16u * (uint32_t)j;                // byte offset of group kf2 / 16
@@ -1271,17 +1290,24 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 ensure_chunk(c);
                 if (!active) continue;
                 if (slots) {
-                    sweep(c, [&](int v, bool, int k2) {
-                              *(uint16_t*)(lb0 + ring_at(k2, lane_off)) = (uint16_t)v;
-                          },
-                          [&](int k2) {
-                              // k2 - kf2 <= 32 here: at most two groups to store
-                              if (k2 > klim) {
-                                  store_group();
-                                  if (k2 - kf2 >= 16) store_group();
-                              }
-                          },
-                          [&](int k2) { flush(k2); });
+                    auto on_step = [&](int k2) {
+                        // k2 - kf2 <= 32 here: at most two groups to store
+                        if (k2 > klim) {
+                            store_group();
+                            if (k2 - kf2 >= 16) store_group();
+                        }
+                    };
+                    auto on_row = [&](int k2) { flush(k2); };
+                    // slot entries are byte offsets in the whole region: chunk 1's entries
+                    // follow chunk 0's kCap
+                    if (c == 0)
+                        sweep(c, [&](int v, bool, int k2) {
+                                  *(uint16_t*)(lb0 + ring_at(k2, lane_off)) = (uint16_t)v;
+                              }, on_step, on_row);
+                    else
+                        sweep(c, [&](int v, bool, int k2) {
+                                  *(uint16_t*)(lb0 + ring_at(k2, lane_off)) = (uint16_t)(v + 16 * kCap);
+                              }, on_step, on_row);
                 } else {
                     sweep(c, [&](int, bool, int) {}, none, none);
                 }
@@ -1306,21 +1332,23 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         const int mycnt = active ? a.cnt[j] : 0;
         int btot;
         const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
-        if (one_chunk) {
-            // targets with more than K neighbours: the rest by a second sweep
+        if (slotted) {
+            // targets with more than K neighbours: the rest by a second sweep (over both
+            // chunks of a two-chunk region, k counting on as in the count pass)
             const bool over = active && mycnt > a.K;
             if (block_any<kBlock>(over, sh.w32)) {
-                ensure_chunk(0);
-                if (over) {
-                    const int64_t base = ebase + ex;
-                    sweep(0, [&](int vb, bool e, int k2) {
-                        const int k = k2 >> 1, v = vb >> 4;
-                        if (e && k >= a.K && k < mycnt) {
-                            const uint32_t Tp = sh.T[v];
-                            emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
-                                      unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
-                        }
-                    }, none, none);
+                const int64_t base = ebase + ex;
+                for (int c = 0; c < nchunks; ++c) {
+                    ensure_chunk(c);
+                    if (over)
+                        sweep(c, [&](int vb, bool e, int k2) {
+                            const int k = k2 >> 1, v = vb >> 4;
+                            if (e && k >= a.K && k < mycnt) {
+                                const uint32_t Tp = sh.T[v];
+                                emit_edge(a, base + k, __float_as_int(shq[v].w), my_id,
+                                          unpack3(Tp, 0) + fx, unpack3(Tp, 1) + fy, unpack3(Tp, 2) + fz);
+                            }
+                        }, none, none);
                 }
             }
         } else {
@@ -1348,7 +1376,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         int64_t tt;
         block_excl_scan<int64_t, kBlock>(tile_found, sh.w64, &tt);
         const bool over = block_any<kBlock>(over_any, sh.w32);
-        const int fix = (over ? kFixOver : 0) | ((one_chunk && a.slot != nullptr) ? 0 : kFixChunked);
+        const int fix = (over ? kFixOver : 0) | (slotted ? (nchunks == 2 ? kFix2 : 0) : kFixChunked);
         out.tt = tt;
         out.fix = fix;
         if (MODE == 0 && threadIdx.x == 0) {
@@ -1359,27 +1387,19 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
     return out;
 }
 
-// MODE 0 (count) and MODE 1 (fix-up write): one tile per workgroup.
-template <int MODE>
-__global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
+// Writes every edge the count pass left in the slots of tile ord (output order), from a
+// region staged for up to CAP entries: kCap for most tiles (expand_kernel), 2 kCap for the
+// two-chunk tiles (inside search_kernel<1>).
+template <int CAP>
+__device__ __forceinline__ void expand_one(const SearchArgs& a, typename ExpandLdsOf<CAP>::type& sh,
+                                           int64_t ord)
 {
-    __shared__ typename LdsOf<MODE>::type sh;
-    search_tile<MODE>(a, sh, blockIdx.x);
-}
-
-// Writes every edge held in the count pass's slots, one workgroup per tile (the write
-// stage of the two-stage build; tiles whose region needs several LDS chunks are left to
-// search_kernel<1>).
-__global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
-{
-    __shared__ ExpandLds sh;
-    const int64_t ord = blockIdx.x;  // output order, as search_kernel
     const int64_t rank = xcd_tile_rank(ord, a.ntiles);
     const int* tstart = a.subset ? a.tbstart : a.bstart;
     const int64_t kb = rank * a.tb;
     const int tbeg = tstart[kb], tend = tstart[kb + a.tb];
     const int ntg = tend - tbeg;
-    if (ntg == 0 || (a.tfix[ord] & kFixChunked)) return;
+    if (ntg == 0) return;
     const int64_t ebase = a.tbase[ord];
     if (ebase + a.ttot[ord] > a.capacity) {
         if (threadIdx.x == 0)
@@ -1389,11 +1409,43 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
     const int lin = a.tile_of_rank[rank];
     const int g0[3] = {(lin % a.ntl[0]) * a.T[0], ((lin / a.ntl[0]) % a.ntl[1]) * a.T[1],
                        (lin / (a.ntl[0] * a.ntl[1])) * a.T[2]};
-    stage_pairs(a, sh, g0);
+    stage_pairs<CAP>(a, sh, g0);
     if (!a.out_vec && !a.out_dist)
-        expand_tile<true>(a, sh, tbeg, ntg, ebase);
+        expand_tile<true, CAP>(a, sh, tbeg, ntg, ebase);
     else
-        expand_tile<false>(a, sh, tbeg, ntg, ebase);
+        expand_tile<false, CAP>(a, sh, tbeg, ntg, ebase);
+}
+
+// MODE 0 (count) and MODE 1 (fix-up write): one tile per workgroup.  The fix-up also
+// expands the slots of the two-chunk tiles (their region needs the larger staging buffer).
+template <int MODE>
+__global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
+{
+    if constexpr (MODE == 0) {
+        __shared__ CountLds sh;
+        search_tile<0>(a, sh, blockIdx.x);
+    } else {
+        __shared__ union {
+            FixLds f;
+            Expand2Lds e;
+        } u;
+        if (a.tfix[blockIdx.x] & kFix2) {
+            expand_one<2 * kCap>(a, u.e, blockIdx.x);
+            __syncthreads();
+        }
+        search_tile<1>(a, u.f, blockIdx.x);
+    }
+}
+
+// Writes every edge held in the count pass's slots, one workgroup per tile (the write
+// stage of the two-stage build; tiles whose region needs two LDS chunks are expanded by
+// search_kernel<1>, larger ones written by it directly).
+__global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
+{
+    __shared__ ExpandLds sh;
+    const int64_t ord = blockIdx.x;  // output order, as search_kernel
+    if (a.tfix[ord] & (kFixChunked | kFix2)) return;
+    expand_one<kCap>(a, sh, ord);
 }
 
 // ---------------------------------------------------------------- all-pairs fallback

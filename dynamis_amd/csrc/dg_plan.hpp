@@ -228,7 +228,9 @@ inline void plan_grid(Plan& p)
                             p.C[1] * (p.C[3] * p.C[8] - p.C[5] * p.C[6]) +
                             p.C[2] * (p.C[3] * p.C[7] - p.C[4] * p.C[6]));
     const double deg = (double)p.n / vol * (4.0 / 3.0) * 3.14159265358979 * p.r * p.r * p.r;
-    double k = 1.3 * deg + 32.0;
+    // (1.5x + 48: the headroom also covers a density up to about twice the mean in part
+    // of the cell, as in a two-phase slab; unused groups of a slot are never touched)
+    double k = 1.5 * deg + 48.0;
     k = std::min(std::max(k, 32.0), 2048.0);
     p.K = ((int)k + 7) & ~7;
 }

@@ -302,3 +302,22 @@ def test_near_coincident_atoms(cuda, dtype, shape):
     # reference writes it), none at or below it
     thr = float(np.float32(1e-8))
     assert np.all(d2 > thr) and np.sum(d2 < 1.03 * thr) > 1000
+
+
+def _two_phase(side, rho_lo, rho_hi, seed):
+    rng = np.random.default_rng(seed)
+    cell = np.eye(3) * side
+    vol = side ** 3
+    f_lo = rng.uniform(0, 1, (int(rho_lo * vol / 2), 3)) * [1, 1, 0.5]
+    f_hi = rng.uniform(0, 1, (int(rho_hi * vol / 2), 3)) * [1, 1, 0.5] + [0, 0, 0.5]
+    return (np.concatenate([f_lo, f_hi]) @ cell).astype(np.float32), cell
+
+
+@pytest.mark.parametrize("side,rho_lo,rho_hi,r", [(60.0, 0.2, 0.02, 6.0), (50.0, 0.3, 0.01, 5.0)])
+def test_two_phase_dense_tiles(cuda, side, rho_lo, rho_hi, r):
+    """A two-phase box: tiles are planned for the mean density, so in the dense phase the
+    region needs two LDS chunks (slots over both chunks, expanded by the fix-up kernel) and
+    many targets exceed the slot capacity (their edges k >= K swept again across both
+    chunks)."""
+    pos, cell = _two_phase(side, rho_lo, rho_hi, 5)
+    check_parity(pos, cell, (1, 1, 1), r, cuda, name=f"two-phase {side} {rho_lo}/{rho_hi}")
