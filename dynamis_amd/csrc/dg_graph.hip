@@ -28,7 +28,10 @@
 #include <stdlib.h>
 #include <string.h>
 
+#include <mutex>
 #include <string>
+#include <utility>
+#include <vector>
 
 #include "../../include/dynamis_graph.h"
 #include "dg_common.hpp"
@@ -1689,6 +1692,20 @@ BruteArgs brute_args(const Plan& p, const void* pos, const int64_t* tgt, void* w
     return b;
 }
 
+// Dynamic LDS beyond the default 64 KiB for kernel fn (gfx950 allows up to 160 KiB per
+// workgroup); the attribute is raised once per kernel and size.
+static void allow_dyn_lds(const void* fn, size_t bytes)
+{
+    if (bytes <= 65536) return;
+    static std::mutex mu;
+    static std::vector<std::pair<const void*, size_t>> done;
+    std::lock_guard<std::mutex> lock(mu);
+    for (auto& d : done)
+        if (d.first == fn && d.second >= bytes) return;
+    if (hipFuncSetAttribute(fn, hipFuncAttributeMaxDynamicSharedMemorySize, (int)bytes) == hipSuccess)
+        done.emplace_back(fn, bytes);
+}
+
 // Steps 1-5 of a build: Morton tile ranks, counting sort of the atoms (and of the
 // explicit targets) into the SFC-ordered cell list.
 void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void* ws,
@@ -1712,6 +1729,8 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         // 3-5. tile buckets, then each tile's bins in LDS
         const unsigned nch = (unsigned)std::max<int64_t>(1, std::min<int64_t>(kSortChunks, (p.n + 4095) / 4096));
         const size_t hl = 4 * (size_t)p.ntiles;
+        allow_dyn_lds((const void*)tile_hist_kernel, hl);
+        allow_dyn_lds((const void*)tile_scatter_kernel, hl);
         hipLaunchKernelGGL(tile_hist_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
                            (const uint32_t*)at<uint32_t>(ws, p.o_key), tcnt, wgb);
         hipLaunchKernelGGL(tile_scatter_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,

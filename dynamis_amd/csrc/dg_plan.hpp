@@ -19,7 +19,7 @@ namespace dg {
 
 constexpr int kBlock = 256;      // threads per search workgroup (4 x wave64)
 constexpr int kSortChunks = 64;      // atom chunks of the tile-level counting sort
-constexpr int kSortTilesMax = 16000;  // tiles it handles (an LDS histogram of ints, < 64 KiB)
+constexpr int kSortTilesMax = 36000;  // tiles it handles (an LDS histogram of ints, < 144 KiB)
 constexpr int kMaxRegion = 768;  // region bins staged per tile
 constexpr int kTileTargets = 235; // aim: targets per tile <= this (a 256-lane workgroup)
 constexpr int kTileMax = 6;

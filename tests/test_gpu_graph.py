@@ -156,6 +156,24 @@ def test_c5_partition_small(cuda):
     check_parity(box.pos, box.cell, box.pbc, box.radius, cuda, targets=box.targets, name="C5 small")
 
 
+def test_c5_full_size_counts(cuda):
+    """C5 at full size (4.4M atoms, 4M owned targets): 21600 tiles, past the 16000 of one
+    64 KiB LDS histogram, so the tile-level sort runs with its larger LDS.  Per-target
+    degrees against the oracle's (counts only: the 3.6e8 edges would not fit the oracle's
+    memory), and the edge count equals their sum."""
+    box = configs.c5()
+    _announce(f"C5 full N={len(box.pos)} targets={len(box.targets)}")
+    pt = torch.from_numpy(box.pos).to(cuda)
+    tt = torch.from_numpy(box.targets).to(cuda)
+    c = torch.from_numpy(np.asarray(box.cell, np.float64))
+    b = torch.tensor(list(box.pbc))
+    cnt = impl.radius_graph_pbc_counts_ex(pt, c, b, box.radius, tt)
+    want, wtot = oracle.radius_graph_counts(box.pos, np.asarray(box.cell, np.float64), box.pbc,
+                                            float(np.float32(box.radius)), target_indices=box.targets)
+    assert np.array_equal(cnt.cpu().numpy(), want)
+    assert int(wtot) == int(want.sum()) > 3e8
+
+
 # ---- design corner cases ----------------------------------------------------------
 def test_wrapped_and_far_positions(cuda):
     cell = np.array([[11.0, 0, 0], [2.0, 12.0, 0], [-1.5, 1.0, 10.0]])
