@@ -30,6 +30,7 @@
 
 #include <mutex>
 #include <string>
+#include <type_traits>
 #include <utility>
 #include <vector>
 
@@ -332,25 +333,48 @@ struct TileSortLds {
     int w32[4];
 };
 
-// One workgroup per tile: orders its bucket by (bin, atom id), writes the tile's bin starts
-// and its part of the cell list.  Each entry's record is gathered into registers as soon as
+// What tile_sort_kernel writes for one sorted entry.  Atoms (TGT false): the cell-list
+// record (position in the bin and id, floor, id, and the inverse map); ids are atom ids.
+// Explicit targets (TGT true): ids are caller positions t; the caller position and the
+// cell-list index of target t's atom.
+struct TileSortOut {
+    const float4* rec;  // atoms: records by atom id
+    float4* spos;
+    uint32_t* sflr;
+    int* sid;
+    int* inv;           // atoms: written when given; targets: read (atom -> cell-list index)
+    const int64_t* tgt; // targets: atom of each caller position
+    int64_t natoms;
+    int* tslot;
+    int* tsidx;
+};
+
+// One workgroup per tile: orders its bucket by (bin, id), writes the tile's bin starts and
+// its part of the sorted list.  Each entry's payload is gathered into registers as soon as
 // its id is known, so the gathers overlap the ordering in LDS.
+template <bool TGT>
 __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64_t ntiles,
                                                         const int* __restrict__ tstart,
                                                         const uint64_t* __restrict__ bucket,
-                                                        const float4* __restrict__ rec,
-                                                        int* __restrict__ bstart,
-                                                        float4* __restrict__ spos,
-                                                        uint32_t* __restrict__ sflr,
-                                                        int* __restrict__ sid, int* __restrict__ inv)
+                                                        int* __restrict__ bstart, TileSortOut o)
 {
     __shared__ TileSortLds S;
+    typedef typename std::conditional<TGT, int, float4>::type Pay;
+    auto gather = [&](int i) -> Pay {
+        if constexpr (TGT) {
+            int64_t at = o.tgt[i];
+            at = at < 0 || at >= o.natoms ? 0 : at;  // (out of range: flagged by target_keys_kernel)
+            return o.inv[at];
+        } else {
+            return o.rec[i];
+        }
+    };
     const int64_t r = blockIdx.x;
     const int base = tstart[r], m = tstart[r + 1] - base;
     const bool fits = m <= kTileSortCap;
     for (int l = threadIdx.x; l < tb; l += 256) S.cnt[l] = 0;
     __syncthreads();
-    float4 q[kTileSortPer];
+    Pay q[kTileSortPer];
     int qi[kTileSortPer], ql[kTileSortPer];
 #pragma unroll
     for (int u = 0; u < kTileSortPer; ++u) {
@@ -360,7 +384,7 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
             const uint64_t w = bucket[base + e];
             qi[u] = (int)(uint32_t)w;
             ql[u] = (int)(w >> 32);
-            q[u] = rec[qi[u]];
+            q[u] = gather(qi[u]);
             S.id[e] = qi[u];
             S.lb[e] = ql[u];
             atomicAdd(&S.cnt[ql[u]], 1);
@@ -385,18 +409,23 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
         }
     }
     __syncthreads();
-    auto emit = [&](int d, int i, float4 v) {
-        spos[d] = make_float4(v.x, v.y, v.z, __int_as_float(i));
-        sflr[d] = __float_as_uint(v.w);
-        sid[d] = i;
-        if (inv) inv[i] = d;
+    auto emit = [&](int d, int i, Pay v) {
+        if constexpr (TGT) {
+            o.tslot[d] = i;
+            o.tsidx[d] = v;
+        } else {
+            o.spos[d] = make_float4(v.x, v.y, v.z, __int_as_float(i));
+            o.sflr[d] = __float_as_uint(v.w);
+            o.sid[d] = i;
+            if (o.inv) o.inv[i] = d;
+        }
     };
     if (!fits) {
-        // a very dense tile: bins in arrival order, records gathered from rec
+        // a very dense tile: bins in arrival order, payloads gathered here
         for (int e = threadIdx.x; e < m; e += 256) {
             const uint64_t w = bucket[base + e];
             const int i = (int)(uint32_t)w;
-            emit(base + atomicAdd(&S.cnt[(int)(w >> 32)], 1), i, rec[i]);
+            emit(base + atomicAdd(&S.cnt[(int)(w >> 32)], 1), i, gather(i));
         }
         return;
     }
@@ -416,6 +445,25 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
 }
 
 // ---------------------------------------------------------------- explicit targets
+// Bin key of every target's atom (tile-level sort of the targets); out-of-range targets
+// are flagged and take atom 0.  Also clears the tile totals for the targets' histogram.
+__global__ void target_keys_kernel(int64_t nt, int64_t n, const int64_t* __restrict__ tgt,
+                                   const uint32_t* __restrict__ key, uint32_t* __restrict__ tkey,
+                                   int* __restrict__ tcnt, int64_t ntiles, int64_t* __restrict__ totals)
+{
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    for (int64_t r = i0; r < ntiles; r += stride) tcnt[r] = 0;
+    for (int64_t t = i0; t < nt; t += stride) {
+        int64_t a = tgt[t];
+        if (a < 0 || a >= n) {
+            atomicOr((unsigned long long*)&totals[1], (unsigned long long)DG_FLAG_TARGET);
+            a = 0;
+        }
+        tkey[t] = key[a];
+    }
+}
+
 __global__ void bin_targets_kernel(int64_t nt, int64_t n, const int64_t* __restrict__ tgt,
                                    const uint32_t* __restrict__ key, uint32_t* __restrict__ tkey,
                                    uint32_t* __restrict__ trank, int* __restrict__ tbcnt,
@@ -1736,11 +1784,40 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         hipLaunchKernelGGL(tile_scatter_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
                            (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)tcnt, tstart,
                            (const int*)wgb, at<uint64_t>(ws, p.o_arr));
-        hipLaunchKernelGGL(tile_sort_kernel, dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n, p.tb,
-                           p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_arr),
-                           (const float4*)at<float4>(ws, p.o_rec), bstart, at<float4>(ws, p.o_spos),
-                           at<uint32_t>(ws, p.o_sflr), at<int>(ws, p.o_sid),
-                           p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr);
+        TileSortOut o;
+        memset(&o, 0, sizeof o);
+        o.rec = at<float4>(ws, p.o_rec);
+        o.spos = at<float4>(ws, p.o_spos);
+        o.sflr = at<uint32_t>(ws, p.o_sflr);
+        o.sid = at<int>(ws, p.o_sid);
+        o.inv = p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr;
+        hipLaunchKernelGGL(tile_sort_kernel<false>, dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n, p.tb,
+                           p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_arr), bstart, o);
+        if (p.subset) {
+            // the explicit targets through the same tile-level sort: keyed by their atom's
+            // bin, ordered by caller position inside a bin
+            uint32_t* tkey = at<uint32_t>(ws, p.o_tkey);
+            hipLaunchKernelGGL(target_keys_kernel, dim3((unsigned)std::min<int64_t>(nblocks(std::max(p.nt, p.ntiles)), 4096)),
+                               dim3(256), 0, s, p.nt, p.n, target_idx, (const uint32_t*)at<uint32_t>(ws, p.o_key),
+                               tkey, tcnt, p.ntiles, totals);
+            const unsigned tch = (unsigned)std::max<int64_t>(1, std::min<int64_t>(kSortChunks, (p.nt + 4095) / 4096));
+            hipLaunchKernelGGL(tile_hist_kernel, dim3(tch), dim3(1024), hl, s, p.nt, p.tb, p.ntiles,
+                               (const uint32_t*)tkey, tcnt, wgb);
+            hipLaunchKernelGGL(tile_scatter_kernel, dim3(tch), dim3(1024), hl, s, p.nt, p.tb, p.ntiles,
+                               (const uint32_t*)tkey, (const int*)tcnt, tstart, (const int*)wgb,
+                               at<uint64_t>(ws, p.o_tarr));
+            TileSortOut ot;
+            memset(&ot, 0, sizeof ot);
+            ot.inv = at<int>(ws, p.o_inv);
+            ot.tgt = target_idx;
+            ot.natoms = p.n;
+            ot.tslot = at<int>(ws, p.o_tslot);
+            ot.tsidx = at<int>(ws, p.o_tsidx);
+            hipLaunchKernelGGL(tile_sort_kernel<true>, dim3((unsigned)p.ntiles), dim3(256), 0, s, p.nt, p.tb,
+                               p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_tarr),
+                               at<int>(ws, p.o_tbstart), ot);
+        }
+        return;
     } else {
     // 1. Morton rank of the tiles (and cleared bin counts)
     hipLaunchKernelGGL(tile_rank_kernel, dim3((unsigned)std::min<int64_t>(nblocks(p.nbins), 2048)), dim3(256),

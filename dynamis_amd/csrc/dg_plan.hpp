@@ -48,6 +48,7 @@ struct Plan {
     size_t o_key, o_rank, o_rec, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
     size_t o_arr, o_tor, o_rot;  // o_arr: cell-list ids in arrival order (before the in-bin sort)
     size_t o_tcnt, o_tstart, o_wgb;  // tile-level counting sort: tile totals, starts, chunk bases
+    size_t o_tarr;                   // the same sort of explicit targets: their tile buckets
     size_t o_tkey, o_trank, o_tbcnt, o_tbstart, o_tslot, o_tsidx, o_tcaller;
     size_t o_cnt, o_ttot, o_tfix, o_tbase, o_part, o_tot, o_slot;
     int K = 0;              // neighbour slot entries per target
@@ -262,6 +263,7 @@ inline void plan_layout(Plan& p)
     p.o_tbcnt = take(p.subset ? 4 * nbins : 0);
     p.o_tbstart = take(p.subset ? 4 * (nbins + 1) : 0);
     p.o_tslot = take(p.subset ? 4 * nt : 0);
+    p.o_tarr = take(p.subset ? 8 * nt : 0);
     p.o_tsidx = take(p.subset ? 4 * nt : 0);
     p.o_tcaller = take(p.subset ? 4 * nt : 0);
     p.o_cnt = take(4 * nt);
