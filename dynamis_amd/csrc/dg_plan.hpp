@@ -18,7 +18,10 @@
 namespace dg {
 
 constexpr int kBlock = 256;      // threads per search workgroup (4 x wave64)
-constexpr int kSortChunks = 64;      // atom chunks of the tile-level counting sort
+#ifndef DG_SORT_CHUNKS
+#define DG_SORT_CHUNKS 128
+#endif
+constexpr int kSortChunks = DG_SORT_CHUNKS;  // atom chunks of the tile-level counting sort
 constexpr int kSortTilesMax = 36000;  // tiles it handles (an LDS histogram of ints, < 144 KiB)
 constexpr int kMaxRegion = 768;  // region bins staged per tile
 constexpr int kTileTargets = 235; // aim: targets per tile <= this (a 256-lane workgroup)
