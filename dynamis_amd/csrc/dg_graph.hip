@@ -56,6 +56,10 @@ constexpr int kExpandIlp = 4;  // 64-edge steps per iteration of the expansion (
 constexpr int kFixOver = 1;     // a target has more than K neighbours
 constexpr int kFixChunked = 2;  // the region needs more than two LDS chunks (or no slots)
 constexpr int kFix2 = 4;        // the region needs two LDS chunks (slots hold both)
+#ifndef DG_FIXGRID
+#define DG_FIXGRID 512
+#endif
+constexpr int64_t kFixGrid = DG_FIXGRID;  // workgroups of the fix-up pass (it loops over the tiles)
 
 // Value known to be uniform across the wave, moved to a scalar register.
 __device__ __forceinline__ int rfl(int x) { return __builtin_amdgcn_readfirstlane(x); }
@@ -1480,11 +1484,17 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             FixLds f;
             Expand2Lds e;
         } u;
-        if (a.tfix[blockIdx.x] & kFix2) {
-            expand_one<2 * kCap>(a, u.e, blockIdx.x);
-            __syncthreads();
+        // a grid of at most DG_FIXGRID workgroups walks the tiles: most have nothing to do
+        for (int64_t ord = blockIdx.x; ord < a.ntiles; ord += gridDim.x) {
+            const int fix = a.tfix[ord];
+            if (fix == 0) continue;
+            if (fix & kFix2) {
+                expand_one<2 * kCap>(a, u.e, ord);
+                __syncthreads();
+            }
+            search_tile<1>(a, u.f, ord);
+            __syncthreads();  // before the next tile reuses the LDS
         }
-        search_tile<1>(a, u.f, blockIdx.x);
     }
 }
 
@@ -1959,7 +1969,7 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
     a.out_vec = edge_vec; a.out_dist = edge_dist; a.vout_f64 = vec_dtype == DG_F64;
     a.capacity = capacity;
     hipLaunchKernelGGL(expand_kernel, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
-    hipLaunchKernelGGL(search_kernel<1>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    hipLaunchKernelGGL(search_kernel<1>, dim3((unsigned)std::min<int64_t>(p.ntiles, kFixGrid)), dim3(kBlock), 0, s, a);
     return check_launch("dg_graph_write");
 }
 
