@@ -339,3 +339,17 @@ def test_two_phase_dense_tiles(cuda, side, rho_lo, rho_hi, r):
     chunks)."""
     pos, cell = _two_phase(side, rho_lo, rho_hi, 5)
     check_parity(pos, cell, (1, 1, 1), r, cuda, name=f"two-phase {side} {rho_lo}/{rho_hi}")
+
+
+@pytest.mark.parametrize("side,cube,rho_bg,rho_c", [(60.0, 24.0, 0.005, 0.5), (64.0, 26.0, 0.004, 0.45)])
+def test_dense_cube_in_sparse_box(cuda, side, cube, rho_bg, rho_c):
+    """A dense cube in a sparse periodic box, r = 5: tiles are planned for the mean
+    density, so around the cube regions need two, three or four LDS chunks, and the cube's
+    targets have several times the slot capacity K.  Covers every fix-up path: targets past
+    K in one- and two-chunk regions (slots, then a second sweep across the chunks) and in
+    regions of more than two chunks (written directly, chunk by chunk)."""
+    rng = np.random.default_rng(11)
+    bg = rng.uniform(0, side, (int(rho_bg * side ** 3), 3))
+    cl = rng.uniform(0, cube, (int(rho_c * cube ** 3), 3)) + (side - cube) / 2
+    pos = np.concatenate([bg, cl]).astype(np.float32)
+    check_parity(pos, np.eye(3) * side, (1, 1, 1), 5.0, cuda, name=f"dense cube {cube} in {side}")
