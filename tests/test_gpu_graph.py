@@ -224,8 +224,21 @@ def test_deterministic_bytes(cuda):
     assert torch.equal(a[0], z[0]) and torch.equal(a[1], z[1])
 
 
-def test_edge_vectors(cuda):
-    box = configs.c4(scale=0.4)
+def _two_phase_box():
+    class B:
+        pass
+    b = B()
+    b.pos, b.cell = _two_phase(50.0, 0.3, 0.01, 5)
+    b.pbc, b.radius = (1, 1, 1), 5.0
+    return b
+
+
+@pytest.mark.parametrize("which", ["c4", "two-phase"])
+def test_edge_vectors(cuda, which):
+    """Edge vectors and distances (fp64 bit-identical to the canonical formula, fp32 the
+    correctly rounded values); the two-phase box has two-chunk tiles, whose edges come from
+    the fix-up kernel's expansion."""
+    box = configs.c4(scale=0.4) if which == "c4" else _two_phase_box()
     r = box.radius
     o = oracle.radius_graph(box.pos, box.cell, box.pbc, r, vectors=True)
     want = oracle.canonical_sort(o["src"], o["dst"], o["shift"], o["vec"], np.sqrt(o["d2"]))
