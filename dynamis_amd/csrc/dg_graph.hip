@@ -516,9 +516,10 @@ struct SearchArgs {
     double hC[9];  // bin step vectors: row d = C[d] / nb[d]
     double r2;
     int lowtri;    // lower-triangular cell (a along x, b in the xy plane, positive diagonal):
-                   // stencil rows are trimmed to the padded cutoff sphere
+                   // stencil rows are trimmed to the padded cutoff sphere; 2: orthorhombic
     float hax, hbx, hby, hcx, hcy, hcz;  // bin step vectors C[d] / nb[d] (lower triangle)
     float rprune2, pmargin;
+    float gy_off, gz_off;             // -hby - pmargin, -hcz - pmargin (orthorhombic rows)
     float inv_hax, inv_hby, inv_hcz;  // reciprocals of the diagonal bin steps
     int nb[3], P[3], T[3], ntl[3], R[3], pbc[3];
     int tb, nregion;
@@ -1202,6 +1203,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         // inside the trimming margin pmargin)
         const float Oz = uz * a.inv_hcz, Oy = (uy - Oz * a.hcy) * a.inv_hby,
                     Ox = (ux - Oy * a.hbx - Oz * a.hcx) * a.inv_hax;
+        const float Oxp = Ox + (float)a.P[0];  // (orthorhombic rows: x bins from the region's first)
 
         // Sweep this lane's target over the resident chunk c, in the fixed order (dz, dy,
         // x, atom) -- ascending region index; on_cand(v, edge, k) receives every candidate's
@@ -1220,7 +1222,20 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             const int oz = ri / nry, oy = ri - oz * nry;
             int xlo = 0, xhi = nrx - 1;
             va = vb = 0;
-            if (a.lowtri) {
+            if (a.lowtri == 2) {
+                // orthorhombic: the row's bins span y in [py, py + 1] hby and z in
+                // [pz, pz + 1] hcz around the target; their gaps (less the margin) bound the
+                // distance from below, and the x range follows without shear
+                const float py = (float)(oy - a.P[1]) - Oy, pz = (float)(oz - a.P[2]) - Oz;
+                const float gy = fmaxf(fmaxf(fmaf(py, a.hby, -a.pmargin), fmaf(-py, a.hby, a.gy_off)), 0.f);
+                const float gz = fmaxf(fmaxf(fmaf(pz, a.hcz, -a.pmargin), fmaf(-pz, a.hcz, a.gz_off)), 0.f);
+                const float rem2 = fmaf(-gz, gz, fmaf(-gy, gy, a.rprune2));
+                if (rem2 < 0.f) return;
+                const float rem = __builtin_amdgcn_sqrtf(rem2);
+                xlo = max((int)floorf(fmaf(-rem, a.inv_hax, Oxp)), 0);
+                xhi = min((int)floorf(fmaf(rem, a.inv_hax, Oxp)), nrx - 1);
+                if (xlo > xhi) return;
+            } else if (a.lowtri) {
                 // bounding box of the row (bins py, pz relative to the target's bin, all x)
                 // in Cartesian y and z, from the target: its gaps gy, gz bound the distance
                 // from below; the x range that the (padded) cutoff sphere can reach then
@@ -1699,6 +1714,9 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     // cutoff by far more than the fp32 position error
     a.pmargin = (float)(1e-4 * p.r + 1e-3);
     a.rprune2 = (float)((p.r + 2.0 * a.pmargin) * (p.r + 2.0 * a.pmargin));
+    if (a.lowtri && p.C[3] == 0.0 && p.C[6] == 0.0 && p.C[7] == 0.0) a.lowtri = 2;
+    a.gy_off = -a.hby - a.pmargin;
+    a.gz_off = -a.hcz - a.pmargin;
     for (int d = 0; d < 3; ++d) {
         a.nb[d] = p.nb[d]; a.P[d] = p.P[d]; a.T[d] = p.T[d]; a.ntl[d] = p.ntl[d];
         a.R[d] = p.R[d]; a.pbc[d] = p.pbc[d];
