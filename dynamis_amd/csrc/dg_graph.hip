@@ -1943,8 +1943,15 @@ dg_status dg_graph_read_totals(const dg_graph_desc* desc, const void* ws, int64_
     Plan p;
     dg_status st = make_plan(desc, p);
     if (st != DG_OK) return st;
-    int64_t h[2] = {0, 0};
-    hipError_t e = hipMemcpyAsync(h, at<int64_t>((void*)ws, p.o_tot), sizeof h, hipMemcpyDeviceToHost, s);
+    // a small pinned buffer per host thread (allocated on its first call, kept): the copy
+    // then goes straight to it instead of through a pageable staging path
+    thread_local int64_t* pinned = nullptr;
+    if (!pinned && hipHostMalloc((void**)&pinned, 2 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess)
+        pinned = nullptr;
+    int64_t hbuf[2] = {0, 0};
+    int64_t* h = pinned ? pinned : hbuf;
+    h[0] = h[1] = 0;
+    hipError_t e = hipMemcpyAsync(h, at<int64_t>((void*)ws, p.o_tot), 2 * sizeof(int64_t), hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("read totals: ") + hipGetErrorString(e));
     if (total_edges) *total_edges = h[0];
