@@ -276,12 +276,22 @@ __global__ __launch_bounds__(1024) void tile_hist_kernel(int64_t n, int tb, int6
 // the atoms are read in order, the scattered side is the 8-byte stores.
 // Each workgroup scans the tile totals itself (workgroup 0 also stores the tile starts,
 // with tstart[ntiles] = n, for tile_sort_kernel).
+// A tile-bucket entry: an id and the bin inside the tile (< 256).  32 bits (24 + 8) when
+// every id fits 24 bits, else 64 (32 + 32).
+__device__ __forceinline__ uint32_t bk_pack(uint32_t i, uint32_t l, uint32_t*) { return i | (l << 24); }
+__device__ __forceinline__ uint64_t bk_pack(uint32_t i, uint32_t l, uint64_t*) { return (uint64_t)i | ((uint64_t)l << 32); }
+__device__ __forceinline__ int bk_id(uint32_t w) { return (int)(w & 0xFFFFFFu); }
+__device__ __forceinline__ int bk_id(uint64_t w) { return (int)(uint32_t)w; }
+__device__ __forceinline__ int bk_bin(uint32_t w) { return (int)(w >> 24); }
+__device__ __forceinline__ int bk_bin(uint64_t w) { return (int)(w >> 32); }
+
+template <typename BT>
 __global__ __launch_bounds__(1024) void tile_scatter_kernel(int64_t n, int tb, int64_t ntiles,
                                                             const uint32_t* __restrict__ key,
                                                             const int* __restrict__ tcnt,
                                                             int* __restrict__ tstart,
                                                             const int* __restrict__ wgb,
-                                                            uint64_t* __restrict__ bucket)
+                                                            BT* __restrict__ bucket)
 {
     extern __shared__ int h[];  // this chunk's next place in every tile's bucket
     __shared__ int s_w[1024 / 64];
@@ -320,7 +330,7 @@ __global__ __launch_bounds__(1024) void tile_scatter_kernel(int64_t n, int tb, i
             if (i < hi) {
                 const uint32_t r = k[u] / (uint32_t)tb;
                 const int d = atomicAdd(&h[r], 1);
-                bucket[d] = (uint64_t)(uint32_t)i | ((uint64_t)(k[u] - r * (uint32_t)tb) << 32);
+                bucket[d] = bk_pack((uint32_t)i, k[u] - r * (uint32_t)tb, (BT*)nullptr);
             }
         }
     }
@@ -356,10 +366,10 @@ struct TileSortOut {
 // One workgroup per tile: orders its bucket by (bin, id), writes the tile's bin starts and
 // its part of the sorted list.  Each entry's payload is gathered into registers as soon as
 // its id is known, so the gathers overlap the ordering in LDS.
-template <bool TGT>
+template <bool TGT, typename BT>
 __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64_t ntiles,
                                                         const int* __restrict__ tstart,
-                                                        const uint64_t* __restrict__ bucket,
+                                                        const BT* __restrict__ bucket,
                                                         int* __restrict__ bstart, TileSortOut o)
 {
     __shared__ TileSortLds S;
@@ -385,9 +395,9 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
         const int e = threadIdx.x + 256 * u;
         qi[u] = -1;
         if (fits && e < m) {
-            const uint64_t w = bucket[base + e];
-            qi[u] = (int)(uint32_t)w;
-            ql[u] = (int)(w >> 32);
+            const BT w = bucket[base + e];
+            qi[u] = bk_id(w);
+            ql[u] = bk_bin(w);
             q[u] = gather(qi[u]);
             S.id[e] = qi[u];
             S.lb[e] = ql[u];
@@ -395,7 +405,7 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
         }
     }
     if (!fits)
-        for (int e = threadIdx.x; e < m; e += 256) atomicAdd(&S.cnt[(int)(bucket[base + e] >> 32)], 1);
+        for (int e = threadIdx.x; e < m; e += 256) atomicAdd(&S.cnt[bk_bin(bucket[base + e])], 1);
     __syncthreads();
     // bin starts inside the bucket (tb <= 216: one pass of a 256-thread scan)
     {
@@ -427,9 +437,9 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
     if (!fits) {
         // a very dense tile: bins in arrival order, payloads gathered here
         for (int e = threadIdx.x; e < m; e += 256) {
-            const uint64_t w = bucket[base + e];
-            const int i = (int)(uint32_t)w;
-            emit(base + atomicAdd(&S.cnt[(int)(w >> 32)], 1), i, gather(i));
+            const BT w = bucket[base + e];
+            const int i = bk_id(w);
+            emit(base + atomicAdd(&S.cnt[bk_bin(w)], 1), i, gather(i));
         }
         return;
     }
@@ -1806,12 +1816,19 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         const unsigned nch = (unsigned)std::max<int64_t>(1, std::min<int64_t>(kSortChunks, (p.n + 4095) / 4096));
         const size_t hl = 4 * (size_t)p.ntiles;
         allow_dyn_lds((const void*)tile_hist_kernel, hl);
-        allow_dyn_lds((const void*)tile_scatter_kernel, hl);
+        // 32-bit bucket entries when every id (atom, and target position) fits 24 bits
+        const bool narrow = p.n < (1 << 24) && (!p.subset || p.nt < (1 << 24));
+        allow_dyn_lds(narrow ? (const void*)tile_scatter_kernel<uint32_t> : (const void*)tile_scatter_kernel<uint64_t>, hl);
         hipLaunchKernelGGL(tile_hist_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
                            (const uint32_t*)at<uint32_t>(ws, p.o_key), tcnt, wgb);
-        hipLaunchKernelGGL(tile_scatter_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
-                           (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)tcnt, tstart,
-                           (const int*)wgb, at<uint64_t>(ws, p.o_arr));
+        if (narrow)
+            hipLaunchKernelGGL(tile_scatter_kernel<uint32_t>, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
+                               (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)tcnt, tstart,
+                               (const int*)wgb, at<uint32_t>(ws, p.o_arr));
+        else
+            hipLaunchKernelGGL(tile_scatter_kernel<uint64_t>, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
+                               (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)tcnt, tstart,
+                               (const int*)wgb, at<uint64_t>(ws, p.o_arr));
         TileSortOut o;
         memset(&o, 0, sizeof o);
         o.rec = at<float4>(ws, p.o_rec);
@@ -1819,8 +1836,12 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         o.sflr = at<uint32_t>(ws, p.o_sflr);
         o.sid = at<int>(ws, p.o_sid);
         o.inv = p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr;
-        hipLaunchKernelGGL(tile_sort_kernel<false>, dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n, p.tb,
-                           p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_arr), bstart, o);
+        if (narrow)
+            hipLaunchKernelGGL((tile_sort_kernel<false, uint32_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n,
+                               p.tb, p.ntiles, (const int*)tstart, (const uint32_t*)at<uint32_t>(ws, p.o_arr), bstart, o);
+        else
+            hipLaunchKernelGGL((tile_sort_kernel<false, uint64_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n,
+                               p.tb, p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_arr), bstart, o);
         if (p.subset) {
             // the explicit targets through the same tile-level sort: keyed by their atom's
             // bin, ordered by caller position inside a bin
@@ -1831,9 +1852,14 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
             const unsigned tch = (unsigned)std::max<int64_t>(1, std::min<int64_t>(kSortChunks, (p.nt + 4095) / 4096));
             hipLaunchKernelGGL(tile_hist_kernel, dim3(tch), dim3(1024), hl, s, p.nt, p.tb, p.ntiles,
                                (const uint32_t*)tkey, tcnt, wgb);
-            hipLaunchKernelGGL(tile_scatter_kernel, dim3(tch), dim3(1024), hl, s, p.nt, p.tb, p.ntiles,
-                               (const uint32_t*)tkey, (const int*)tcnt, tstart, (const int*)wgb,
-                               at<uint64_t>(ws, p.o_tarr));
+            if (narrow)
+                hipLaunchKernelGGL(tile_scatter_kernel<uint32_t>, dim3(tch), dim3(1024), hl, s, p.nt, p.tb, p.ntiles,
+                                   (const uint32_t*)tkey, (const int*)tcnt, tstart, (const int*)wgb,
+                                   at<uint32_t>(ws, p.o_tarr));
+            else
+                hipLaunchKernelGGL(tile_scatter_kernel<uint64_t>, dim3(tch), dim3(1024), hl, s, p.nt, p.tb, p.ntiles,
+                                   (const uint32_t*)tkey, (const int*)tcnt, tstart, (const int*)wgb,
+                                   at<uint64_t>(ws, p.o_tarr));
             TileSortOut ot;
             memset(&ot, 0, sizeof ot);
             ot.inv = at<int>(ws, p.o_inv);
@@ -1841,9 +1867,14 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
             ot.natoms = p.n;
             ot.tslot = at<int>(ws, p.o_tslot);
             ot.tsidx = at<int>(ws, p.o_tsidx);
-            hipLaunchKernelGGL(tile_sort_kernel<true>, dim3((unsigned)p.ntiles), dim3(256), 0, s, p.nt, p.tb,
-                               p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_tarr),
-                               at<int>(ws, p.o_tbstart), ot);
+            if (narrow)
+                hipLaunchKernelGGL((tile_sort_kernel<true, uint32_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s,
+                                   p.nt, p.tb, p.ntiles, (const int*)tstart,
+                                   (const uint32_t*)at<uint32_t>(ws, p.o_tarr), at<int>(ws, p.o_tbstart), ot);
+            else
+                hipLaunchKernelGGL((tile_sort_kernel<true, uint64_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s,
+                                   p.nt, p.tb, p.ntiles, (const int*)tstart,
+                                   (const uint64_t*)at<uint64_t>(ws, p.o_tarr), at<int>(ws, p.o_tbstart), ot);
         }
         return;
     } else {
