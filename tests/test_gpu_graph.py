@@ -174,6 +174,40 @@ def test_c5_full_size_counts(cuda):
     assert int(wtot) == int(want.sum()) > 3e8
 
 
+def test_c3_full_size(cuda):
+    """The headline workload at full size (1M atoms, ~9.05e7 edges), through properties
+    that need no full oracle edge list: per-target degrees equal the oracle's (C, exact
+    canonical predicate), dst-degrees of the edge list equal them, every edge is within the
+    cutoff in fp64, and the set is symmetric: (i, j, S) is an edge iff (j, i, -S) is."""
+    box = configs.c3()
+    N = len(box.pos)
+    _announce(f"C3 full N={N}")
+    cell = np.asarray(box.cell, np.float64)
+    ei, co, nn, cnt = _gpu_build(box.pos, cell, box.pbc, box.radius, None, cuda)
+    # the predicate sees the cell rounded to the position dtype, as the API passes it on
+    # (at C3 one pair lies between the two cells' cutoff spheres)
+    cell = cell.astype(box.pos.dtype).astype(np.float64)
+    E = ei.shape[1]
+    r32 = float(np.float32(box.radius))
+    want, wtot = oracle.radius_graph_counts(box.pos, cell, box.pbc, r32)
+    assert np.array_equal(cnt.cpu().numpy(), want)
+    assert E == int(wtot) == int(nn.sum()) > 9e7
+    src, dst = ei[0], ei[1]
+    assert torch.equal(torch.bincount(dst, minlength=N).to(torch.int32), cnt)
+    S = co.to(torch.int64)
+    assert torch.equal(co, S.to(co.dtype)) and int(S.abs().max()) <= 8  # integer-valued shifts
+    p64 = torch.from_numpy(box.pos).to(cuda).to(torch.float64)
+    vec = p64[src] + S.to(torch.float64) @ torch.from_numpy(cell).to(cuda) - p64[dst]
+    d2 = (vec * vec).sum(1)
+    del vec
+    assert float(d2.max()) <= r32 * r32 * (1 + 1e-12) and float(d2.min()) > 0.0
+    del d2, p64
+    sk = (S[:, 0] + 8) * 289 + (S[:, 1] + 8) * 17 + (S[:, 2] + 8)
+    fwd = (src * N + dst) * 4913 + sk
+    rev = (dst * N + src) * 4913 + (4912 - sk)  # -S in the same 17-radix digits
+    assert torch.equal(torch.sort(fwd).values, torch.sort(rev).values)
+
+
 # ---- design corner cases ----------------------------------------------------------
 def test_wrapped_and_far_positions(cuda):
     cell = np.array([[11.0, 0, 0], [2.0, 12.0, 0], [-1.5, 1.0, 10.0]])
