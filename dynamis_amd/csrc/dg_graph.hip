@@ -1977,8 +1977,10 @@ dg_status dg_graph_read_totals(const dg_graph_desc* desc, const void* ws, int64_
     // a small pinned buffer per host thread (allocated on its first call, kept): the copy
     // then goes straight to it instead of through a pageable staging path
     thread_local int64_t* pinned = nullptr;
-    if (!pinned && hipHostMalloc((void**)&pinned, 2 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess)
+    if (!pinned && hipHostMalloc((void**)&pinned, 2 * sizeof(int64_t), hipHostMallocDefault) != hipSuccess) {
         pinned = nullptr;
+        (void)hipGetLastError();  // (the pageable fallback below; no stale error for later checks)
+    }
     int64_t hbuf[2] = {0, 0};
     int64_t* h = pinned ? pinned : hbuf;
     h[0] = h[1] = 0;
