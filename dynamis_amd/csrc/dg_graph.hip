@@ -39,8 +39,19 @@
 #include "dg_plan.hpp"
 #include "dg_scan.hpp"
 
+// The count kernel (search_kernel<0>) is compiled in a translation unit of its own,
+// dg_count.hip, which includes this file with DG_COUNT_TU defined: there, only the
+// device code the count kernel needs and its launcher are compiled (under another
+// instruction-scheduling strategy, see build.py), and everything else is left out.
+#ifdef DG_COUNT_TU
+#define DG_MAIN_TU 0
+#else
+#define DG_MAIN_TU 1
+#endif
+
 namespace dg {
 
+#if DG_MAIN_TU
 thread_local std::string g_last_error;
 
 dg_status fail(dg_status st, const std::string& msg)
@@ -48,6 +59,7 @@ dg_status fail(dg_status st, const std::string& msg)
     g_last_error = msg;
     return st;
 }
+#endif
 
 constexpr int kRegPerThread = (kMaxRegion + kBlock - 1) / kBlock;
 constexpr int kBinSortMax = 128;
@@ -82,6 +94,7 @@ struct GridArgs {
     int tb;
 };
 
+#if DG_MAIN_TU
 // ---------------------------------------------------------------- tile SFC ranks
 // Rank of every tile in the compact Morton order (morton_encode) among the tiles of the
 // grid, computed directly: for each 1 bit of the tile's code, the tiles whose codes share
@@ -518,6 +531,8 @@ __global__ void finish_targets_kernel(int64_t nbins, int64_t n, const int* __res
         tsidx[j] = inv[a];
     }
 }
+
+#endif  // DG_MAIN_TU (sort kernels)
 
 // ---------------------------------------------------------------- neighbour search
 struct SearchArgs {
@@ -1523,6 +1538,10 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
     }
 }
 
+#if DG_MAIN_TU
+// the count kernel's launcher, compiled in dg_count.hip
+void launch_count_kernel(const SearchArgs& a, unsigned grid, hipStream_t s);
+
 // Writes every edge held in the count pass's slots, one workgroup per tile (the write
 // stage of the two-stage build; tiles whose region needs two LDS chunks are expanded by
 // search_kernel<1>, larger ones written by it directly).
@@ -1914,10 +1933,18 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
     }
 }
 
+#else   // DG_COUNT_TU
+void launch_count_kernel(const SearchArgs& a, unsigned grid, hipStream_t s)
+{
+    hipLaunchKernelGGL(search_kernel<0>, dim3(grid), dim3(kBlock), 0, s, a);
+}
+#endif  // DG_MAIN_TU
+
 }  // namespace dg
 
 using namespace dg;
 
+#if DG_MAIN_TU
 extern "C" {
 
 const char* dg_last_error(void) { return g_last_error.c_str(); }
@@ -1961,7 +1988,7 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
     // 6. degrees
     SearchArgs a = search_args(p, pos, ws);
     a.counts_user = counts_out;
-    hipLaunchKernelGGL(search_kernel<0>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    launch_count_kernel(a, (unsigned)p.ntiles, s);
     // 7. tile offsets in output order, and the total
     excl_scan<int, int64_t>(at<int>(ws, p.o_ttot), p.ntiles, at<int64_t>(ws, p.o_tbase),
                             at<int64_t>(ws, p.o_part), s, totals);
@@ -2045,3 +2072,4 @@ dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64
 }
 
 }  // extern "C"
+#endif  // DG_MAIN_TU
