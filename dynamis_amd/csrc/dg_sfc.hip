@@ -271,20 +271,16 @@ __device__ __forceinline__ double shift_at(const void* sh, int dt, int64_t k)
     return (double)((const int64_t*)sh)[k];
 }
 
+struct FilterCell {
+    double c[9];
+};
+
 // keep iff canonical d2 <= r^2 (dist_graph_ops_kernels.cu:16-43 keeps d2 <= r2, no lower bound)
-__global__ void filter_flag_kernel(const void* __restrict__ pos, int f64, const double* cellp,
-                                   double r2, const int64_t* __restrict__ src,
-                                   const int64_t* __restrict__ dst, const void* __restrict__ sh,
-                                   int sdt, int64_t E, int* __restrict__ flag, double c0, double c1,
-                                   double c2, double c3, double c4, double c5, double c6, double c7,
-                                   double c8)
+__device__ __forceinline__ bool filter_keep(const void* __restrict__ pos, int f64, const FilterCell& C,
+                                            double r2, int64_t s, int64_t d, const void* __restrict__ sh,
+                                            int sdt, int64_t e)
 {
-    int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (e >= E) return;
-    const double C[9] = {c0, c1, c2, c3, c4, c5, c6, c7, c8};
-    (void)cellp;
     double ps[3], pt[3];
-    const int64_t s = src[e], d = dst[e];
     if (f64) {
         const double* a = (const double*)pos;
         for (int k = 0; k < 3; ++k) { ps[k] = a[3 * s + k]; pt[k] = a[3 * d + k]; }
@@ -296,9 +292,93 @@ __global__ void filter_flag_kernel(const void* __restrict__ pos, int f64, const 
                  S2 = shift_at(sh, sdt, 3 * e + 2);
     double v[3];
     for (int a = 0; a < 3; ++a)
-        v[a] = (ps[a] - pt[a]) + fma(S2, C[6 + a], fma(S1, C[3 + a], S0 * C[a]));
-    double d2 = fma(v[2], v[2], fma(v[1], v[1], v[0] * v[0]));
-    flag[e] = d2 <= r2 ? 1 : 0;
+        v[a] = (ps[a] - pt[a]) + fma(S2, C.c[6 + a], fma(S1, C.c[3 + a], S0 * C.c[a]));
+    const double d2 = fma(v[2], v[2], fma(v[1], v[1], v[0] * v[0]));
+    return d2 <= r2;
+}
+
+__global__ void filter_flag_kernel(const void* __restrict__ pos, int f64, FilterCell C, double r2,
+                                   const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
+                                   const void* __restrict__ sh, int sdt, int64_t E,
+                                   int* __restrict__ flag)
+{
+    int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (e >= E) return;
+    flag[e] = filter_keep(pos, f64, C, r2, src[e], dst[e], sh, sdt, e) ? 1 : 0;
+}
+
+// Two-pass compaction (count, then write in order): a workgroup of 256 threads takes
+// kFilterPer consecutive edges per thread, kFilterTile per workgroup (one edge per thread:
+// each edge's pos gathers depend on its src/dst loads, and with four edges per thread the
+// C3 filter took 6.7 ms instead of 2.9 ms).  Pass 1 stores the
+// workgroup's kept count; pass 2 re-evaluates the predicate and writes the kept edges at
+// the workgroup's offset plus their rank inside it.
+constexpr int kFilterPer = 1;
+constexpr int kFilterTile = 256 * kFilterPer;
+
+__device__ __forceinline__ int filter_tile_flags(const void* pos, int f64, const FilterCell& C,
+                                                 double r2, const int64_t* src, const int64_t* dst,
+                                                 const void* sh, int sdt, int64_t E, int64_t e0,
+                                                 int64_t* s, int64_t* d, bool* keep)
+{
+    int n = 0;
+#pragma unroll
+    for (int k = 0; k < kFilterPer; ++k) {
+        const int64_t e = e0 + k;
+        keep[k] = false;
+        if (e < E) {
+            s[k] = src[e];
+            d[k] = dst[e];
+            keep[k] = filter_keep(pos, f64, C, r2, s[k], d[k], sh, sdt, e);
+        }
+        n += keep[k] ? 1 : 0;
+    }
+    return n;
+}
+
+__global__ __launch_bounds__(256) void filter_count_kernel(const void* __restrict__ pos, int f64,
+                                                           FilterCell C, double r2,
+                                                           const int64_t* __restrict__ src,
+                                                           const int64_t* __restrict__ dst,
+                                                           const void* __restrict__ sh, int sdt,
+                                                           int64_t E, int* __restrict__ bcnt)
+{
+    __shared__ int s_w[4];
+    const int64_t e0 = (int64_t)blockIdx.x * kFilterTile + (int64_t)threadIdx.x * kFilterPer;
+    int64_t s[kFilterPer], d[kFilterPer];
+    bool keep[kFilterPer];
+    const int n = filter_tile_flags(pos, f64, C, r2, src, dst, sh, sdt, E, e0, s, d, keep);
+    int tot;
+    block_excl_scan<int, 256>(n, s_w, &tot);
+    if (threadIdx.x == 0) bcnt[blockIdx.x] = tot;
+}
+
+template <typename ST>
+__global__ __launch_bounds__(256) void filter_write_kernel(const void* __restrict__ pos, int f64,
+                                                           FilterCell C, double r2,
+                                                           const int64_t* __restrict__ src,
+                                                           const int64_t* __restrict__ dst,
+                                                           const ST* __restrict__ sh, int sdt,
+                                                           int64_t E, const int64_t* __restrict__ boff,
+                                                           int64_t* __restrict__ osrc,
+                                                           int64_t* __restrict__ odst,
+                                                           ST* __restrict__ osh)
+{
+    __shared__ int s_w[4];
+    const int64_t e0 = (int64_t)blockIdx.x * kFilterTile + (int64_t)threadIdx.x * kFilterPer;
+    int64_t s[kFilterPer], d[kFilterPer];
+    bool keep[kFilterPer];
+    const int n = filter_tile_flags(pos, f64, C, r2, src, dst, sh, sdt, E, e0, s, d, keep);
+    int tot;
+    int64_t o = boff[blockIdx.x] + block_excl_scan<int, 256>(n, s_w, &tot);
+#pragma unroll
+    for (int k = 0; k < kFilterPer; ++k) {
+        if (!keep[k]) continue;
+        osrc[o] = s[k];
+        odst[o] = d[k];
+        for (int c = 0; c < 3; ++c) osh[3 * o + c] = sh[3 * (e0 + k) + c];
+        ++o;
+    }
 }
 
 __global__ void filter_compact_kernel(const int* __restrict__ flag, const int64_t* __restrict__ pre,
@@ -340,6 +420,24 @@ SortLayout sort_layout(int64_t n)
     L.o_span = take(16);
     L.total = o;
     return L;
+}
+
+FilterCell filter_cell(const double* cell)
+{
+    FilterCell C;
+    for (int k = 0; k < 9; ++k) C.c[k] = cell[k];
+    return C;
+}
+
+dg_status filter_check(int32_t pos_dtype, int32_t shift_dtype, double radius, int64_t E,
+                       int64_t n_atoms)
+{
+    if (pos_dtype != DG_F32 && pos_dtype != DG_F64) return fail(DG_ERR_INVALID, "pos dtype");
+    if (shift_dtype != DG_F32 && shift_dtype != DG_F64 && shift_dtype != DG_I64)
+        return fail(DG_ERR_INVALID, "shift dtype");
+    if (!(radius > 0.0)) return fail(DG_ERR_INVALID, "radius must be positive");
+    if (E < 0 || n_atoms < 0) return fail(DG_ERR_INVALID, "negative size");
+    return DG_OK;
 }
 
 }  // namespace
@@ -468,13 +566,69 @@ dg_status dg_filter_edges_to_radius(const void* pos, int32_t pos_dtype, int64_t 
     int64_t* part = (int64_t*)(w + al(4 * (size_t)E) + al(8 * (size_t)(E + 1)));
     if (E > 0)
         hipLaunchKernelGGL(filter_flag_kernel, dim3(nblk(E)), dim3(256), 0, s, pos,
-                           (int)(pos_dtype == DG_F64), (const double*)nullptr, radius * radius, src,
-                           dst, shift, (int)shift_dtype, E, flag, cell[0], cell[1], cell[2], cell[3],
-                           cell[4], cell[5], cell[6], cell[7], cell[8]);
+                           (int)(pos_dtype == DG_F64), filter_cell(cell), radius * radius, src, dst,
+                           shift, (int)shift_dtype, E, flag);
     device_excl_scan<int, int64_t>(flag, E, pre, part, s);
     hipLaunchKernelGGL(filter_compact_kernel, dim3(E > 0 ? nblk(E) : 1), dim3(256), 0, s,
                        (const int*)flag, (const int64_t*)pre, E, keep_idx, n_kept);
     return launch_ok("dg_filter_edges_to_radius");
+}
+
+size_t dg_filter2_workspace_size(int64_t E)
+{
+    if (E < 0) return 0;
+    const size_t nb = (size_t)((E + kFilterTile - 1) / kFilterTile);
+    return al(4 * (nb + 1)) + al(8 * (nb + 1)) + al(8 * (nb / kScanTile + 2));
+}
+
+dg_status dg_filter_count(const void* pos, int32_t pos_dtype, int64_t n_atoms, const double* cell,
+                          double radius, const int64_t* src, const int64_t* dst, const void* shift,
+                          int32_t shift_dtype, int64_t E, int64_t* n_kept, void* ws, size_t ws_bytes,
+                          hipStream_t s)
+{
+    dg_status st = filter_check(pos_dtype, shift_dtype, radius, E, n_atoms);
+    if (st != DG_OK) return st;
+    if (ws_bytes < dg_filter2_workspace_size(E)) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    const int64_t nb = (E + kFilterTile - 1) / kFilterTile;
+    char* w = (char*)ws;
+    int* bcnt = (int*)w;
+    int64_t* boff = (int64_t*)(w + al(4 * (size_t)(nb + 1)));
+    int64_t* part = (int64_t*)(w + al(4 * (size_t)(nb + 1)) + al(8 * (size_t)(nb + 1)));
+    if (nb > 0)
+        hipLaunchKernelGGL(filter_count_kernel, dim3((unsigned)nb), dim3(256), 0, s, pos,
+                           (int)(pos_dtype == DG_F64), filter_cell(cell), radius * radius, src, dst,
+                           shift, (int)shift_dtype, E, bcnt);
+    excl_scan<int, int64_t>(bcnt, nb, boff, part, s, n_kept);
+    return launch_ok("dg_filter_count");
+}
+
+dg_status dg_filter_write(const void* pos, int32_t pos_dtype, int64_t n_atoms, const double* cell,
+                          double radius, const int64_t* src, const int64_t* dst, const void* shift,
+                          int32_t shift_dtype, int64_t E, const void* ws, size_t ws_bytes,
+                          int64_t* out_src, int64_t* out_dst, void* out_shift, hipStream_t s)
+{
+    dg_status st = filter_check(pos_dtype, shift_dtype, radius, E, n_atoms);
+    if (st != DG_OK) return st;
+    if (ws_bytes < dg_filter2_workspace_size(E)) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    const int64_t nb = (E + kFilterTile - 1) / kFilterTile;
+    if (nb == 0) return DG_OK;
+    const int64_t* boff = (const int64_t*)((const char*)ws + al(4 * (size_t)(nb + 1)));
+    const int f64 = (int)(pos_dtype == DG_F64);
+    const FilterCell C = filter_cell(cell);
+    const double r2 = radius * radius;
+    if (shift_dtype == DG_F32)
+        hipLaunchKernelGGL(filter_write_kernel<float>, dim3((unsigned)nb), dim3(256), 0, s, pos, f64, C,
+                           r2, src, dst, (const float*)shift, (int)shift_dtype, E, boff, out_src,
+                           out_dst, (float*)out_shift);
+    else if (shift_dtype == DG_F64)
+        hipLaunchKernelGGL(filter_write_kernel<double>, dim3((unsigned)nb), dim3(256), 0, s, pos, f64, C,
+                           r2, src, dst, (const double*)shift, (int)shift_dtype, E, boff, out_src,
+                           out_dst, (double*)out_shift);
+    else
+        hipLaunchKernelGGL(filter_write_kernel<int64_t>, dim3((unsigned)nb), dim3(256), 0, s, pos, f64,
+                           C, r2, src, dst, (const int64_t*)shift, (int)shift_dtype, E, boff, out_src,
+                           out_dst, (int64_t*)out_shift);
+    return launch_ok("dg_filter_write");
 }
 
 }  // extern "C"

@@ -228,20 +228,29 @@ def filter_edges_to_radius(edges, cell_shifts, pos, cell, radius):
         sdt = L.DG_I64
     c = cell.detach().to(device="cpu", dtype=pos.dtype).to(torch.float64).contiguous()
     cbuf = (L.ctypes.c_double * 9)(*c.reshape(-1).tolist())
-    wsb = lib.dg_filter_workspace_size(E)
+    wsb = lib.dg_filter2_workspace_size(E)
+    pdt = L.DG_F64 if pos.dtype == torch.float64 else L.DG_F32
+    base = edges.data_ptr()
+    args = (L.ptr(pos), pdt, pos.size(0), cbuf, float(radius), L.ctypes.c_void_p(base),
+            L.ctypes.c_void_p(base + 8 * E), L.ptr(sh), sdt, E)
     with torch.cuda.device(dev):
         s = L.stream_of(dev)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
-        keep = torch.empty(E, dtype=torch.int64, device=dev)
         nk = torch.empty(1, dtype=torch.int64, device=dev)
-        base = edges.data_ptr()
-        L.check(lib.dg_filter_edges_to_radius(
-            L.ptr(pos), L.DG_F64 if pos.dtype == torch.float64 else L.DG_F32, pos.size(0), cbuf,
-            float(radius), L.ctypes.c_void_p(base), L.ctypes.c_void_p(base + 8 * E), L.ptr(sh), sdt,
-            E, L.ptr(keep), L.ptr(nk), L.ptr(ws), wsb, s), "filter_edges_to_radius")
+        # pass 1: kept count per block of edges and their offsets; pass 2 (after the
+        # exact-size allocation): the kept edges, in order, straight into the outputs
+        L.check(lib.dg_filter_count(*args, L.ptr(nk), L.ptr(ws), wsb, s), "filter_edges_to_radius")
         k = int(nk.item())
-        idx = keep[:k]
-        return edges.index_select(1, idx).contiguous(), cell_shifts.index_select(0, idx).contiguous()
+        out_e = torch.empty((2, k), dtype=torch.int64, device=dev)
+        out_s = torch.empty((k, 3), dtype=sh.dtype, device=dev)
+        if k > 0:
+            ob = out_e.data_ptr()
+            L.check(lib.dg_filter_write(*args, L.ptr(ws), wsb, L.ctypes.c_void_p(ob),
+                                        L.ctypes.c_void_p(ob + 8 * k), L.ptr(out_s), s),
+                    "filter_edges_to_radius")
+        if out_s.dtype != cell_shifts.dtype:
+            out_s = out_s.to(cell_shifts.dtype)
+        return out_e, out_s
 
 
 def extract_halo_info(edges, pid_outer, my_outer_atoms, my_rank, world_size, N):

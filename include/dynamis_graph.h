@@ -130,6 +130,25 @@ dg_status dg_filter_edges_to_radius(const void* pos, int32_t pos_dtype, int64_t 
                                     int64_t* n_kept, void* workspace, size_t workspace_bytes,
                                     hipStream_t stream);
 
+/* The same filter as a count / write pair that writes the kept edges themselves (in order,
+ * shifts in shift_dtype), for exact-size outputs without an index gather: the form the
+ * Python filter_edges_to_radius uses.  Replaces the same reference function as above.
+ *   dg_filter_count: n_kept out int64 (device, one value); workspace of
+ *     dg_filter2_workspace_size(n_edges) bytes, kept for dg_filter_write
+ *   dg_filter_write: out_src/out_dst int64 [n_kept], out_shift [n_kept,3] of shift_dtype;
+ *     same inputs and workspace as the dg_filter_count call before it */
+size_t dg_filter2_workspace_size(int64_t n_edges);
+dg_status dg_filter_count(const void* pos, int32_t pos_dtype, int64_t n_atoms, const double* cell,
+                          double radius, const int64_t* edge_src, const int64_t* edge_dst,
+                          const void* cell_shift, int32_t shift_dtype, int64_t n_edges,
+                          int64_t* n_kept, void* workspace, size_t workspace_bytes,
+                          hipStream_t stream);
+dg_status dg_filter_write(const void* pos, int32_t pos_dtype, int64_t n_atoms, const double* cell,
+                          double radius, const int64_t* edge_src, const int64_t* edge_dst,
+                          const void* cell_shift, int32_t shift_dtype, int64_t n_edges,
+                          const void* workspace, size_t workspace_bytes, int64_t* out_src,
+                          int64_t* out_dst, void* out_shift, hipStream_t stream);
+
 /* SFC keys exactly as partition/sfc_kernels.cu:19-109 (curve 0 = Morton 21-bit,
  * 1 = "Hilbert" order 7), normalised by the global min / range of pos
  * (sfc_kernels.cu:196-198, range 0 -> 1).  pos fp32 [n,3]; keys int64 [n];
