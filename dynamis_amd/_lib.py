@@ -73,6 +73,7 @@ def lib():
         "dg_graph_read_totals": (_i32, [D, _p, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _p]),
         "dg_graph_write": (_i32, [D, _p, _p, _p, _sz, _i64, _p, _p, _p, _p, _p, _i32, _p]),
         "dg_graph_build": (_i32, [D, _p, _p, _p, _sz, _i64, _p, _p, _p, _p, _p, _p, _i32, _p]),
+        "dg_graph_build_noalloc": (_i32, [D, _p, _p, _i64, _p, _p, _p, _p, _p, _p, _i32, _p, _p]),
         "dg_filter_workspace_size": (_sz, [_i64]),
         "dg_filter_edges_to_radius": (_i32, [_p, _i32, _i64, _p, ctypes.c_double, _p, _p, _p, _i32,
                                              _i64, _p, _p, _p, _sz, _p]),

@@ -2072,4 +2072,70 @@ dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64
 }
 
 }  // extern "C"
+
+// ---------------------------------------------------------------- allocation-free build
+// A device-resident workspace for dg_graph_build_noalloc: the build's whole workspace
+// (cell list, slots, tile tables, totals) lives in this array, one copy per GPU, held from
+// the library's load until the process ends.  Host code never names the array itself (its
+// host-side symbol is no device address): it uses the address hipGetSymbolAddress
+// returns on each device, kept in g_scratch_ptr.
+namespace dg {
+constexpr size_t kScratchBytes = (size_t)64 << 20;
+constexpr int kMaxDevices = 64;
+static __device__ __align__(256) unsigned char scratch[kScratchBytes];
+static std::mutex g_scratch_mu;
+static void* g_scratch_ptr[kMaxDevices];
+
+// The scratch address on the current device, looked up once per device.
+static dg_status scratch_on_current_device(void** out)
+{
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    if (dev < 0 || dev >= kMaxDevices) return fail(DG_ERR_INVALID, "device ordinal out of range");
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    if (!g_scratch_ptr[dev]) {
+        void* ptr = nullptr;
+        e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
+        if (e != hipSuccess || !ptr)
+            return fail(DG_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        g_scratch_ptr[dev] = ptr;
+    }
+    *out = g_scratch_ptr[dev];
+    return DG_OK;
+}
+
+// Copies the build's {edge count, flags} to the caller's device buffer.
+__global__ void copy_totals_kernel(const int64_t* __restrict__ totals, int64_t* __restrict__ out)
+{
+    if (threadIdx.x < 2) out[threadIdx.x] = totals[threadIdx.x];
+}
+}  // namespace dg
+
+extern "C" dg_status dg_graph_build_noalloc(const dg_graph_desc* desc, const void* pos,
+                                            const int64_t* target_idx, int64_t capacity,
+                                            int32_t* counts_out, int64_t* edge_src,
+                                            int64_t* edge_dst, float* cell_shift, void* edge_vec,
+                                            void* edge_dist, int32_t vec_dtype,
+                                            int64_t* totals_out, hipStream_t s)
+{
+    Plan p;
+    dg_status st = make_plan(desc, p);
+    if (st != DG_OK) return st;
+    if (!totals_out) return fail(DG_ERR_INVALID, "totals_out is NULL");
+    if (p.ws_bytes > kScratchBytes)
+        return fail(DG_ERR_WORKSPACE, "dg_graph_build_noalloc: this build needs " +
+                                          std::to_string(p.ws_bytes) + " bytes of workspace; the static "
+                                          "scratch holds " + std::to_string(kScratchBytes) +
+                                          " (use dg_graph_build with a caller workspace)");
+    void* ws = nullptr;
+    st = scratch_on_current_device(&ws);
+    if (st != DG_OK) return st;
+    st = dg_graph_build(desc, pos, target_idx, ws, kScratchBytes, capacity, counts_out, edge_src,
+                        edge_dst, cell_shift, edge_vec, edge_dist, vec_dtype, s);
+    if (st != DG_OK) return st;
+    hipLaunchKernelGGL(copy_totals_kernel, dim3(1), dim3(64), 0, s,
+                       (const int64_t*)at<int64_t>(ws, p.o_tot), totals_out);
+    return check_launch("dg_graph_build_noalloc");
+}
 #endif  // DG_MAIN_TU

@@ -115,6 +115,25 @@ dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64
                          float* cell_shift, void* edge_vec, void* edge_dist, int32_t vec_dtype,
                          hipStream_t stream);
 
+/* Allocation-free one-call build.  No counterpart in the reference: it is for callers
+ * that cannot allocate device memory (code under HIP graph capture, tight serving loops,
+ * harnesses that forbid hipMalloc).  The same build as dg_graph_build (same kernels, same
+ * outputs in the same order), with the workspace taken from a static device array inside
+ * the library (64 MiB per GPU, held until the process ends) instead of a caller buffer;
+ * it calls no hipMalloc / hipFree.  Builds whose dg_graph_workspace_size() exceeds
+ * 64 MiB (about 150k atoms at 0.1 atoms/A^3 and r = 6 A) are refused with
+ * DG_ERR_WORKSPACE.  The edge count and status flags are copied on the stream to
+ *   totals_out   device int64 [2]: {total_edges, flags (DG_FLAG_*)}
+ * which the caller reads when it needs them (an edge count above `capacity`, or
+ * DG_FLAG_CAPACITY, means the tiles that did not fit were skipped).  Every call on one
+ * GPU shares that GPU's array: calls that overlap on one GPU (two streams, two host
+ * threads) race and must be serialised by the caller. */
+dg_status dg_graph_build_noalloc(const dg_graph_desc* desc, const void* pos,
+                                 const int64_t* target_idx, int64_t capacity, int32_t* counts_out,
+                                 int64_t* edge_src, int64_t* edge_dst, float* cell_shift,
+                                 void* edge_vec, void* edge_dist, int32_t vec_dtype,
+                                 int64_t* totals_out, hipStream_t stream);
+
 /* Order-preserving filter of an edge list to radius (keep iff d2 <= radius^2, canonical
  * fp64 d2).  Replaces filter_edges_to_radius (dist_graph_ops.cpp:5-35,
  * dist_graph_ops_kernels.cu:16-43,62-102).
