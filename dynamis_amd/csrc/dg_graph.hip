@@ -1680,6 +1680,53 @@ dg_status check_launch(const char* what)
     return DG_OK;
 }
 
+// Opt-in stage timer: with RADIUS_PBC_PROFILE set in the environment (the switch of
+// radius_graph_kernels.cu:444-465), a count or write call records a HIP event on its
+// stream at every stage boundary, waits for the last one and prints each stage's time to
+// stderr.  Off (the default) it does nothing: no events, no synchronisation.
+struct StageTimer {
+    static constexpr int kMax = 8;
+    hipEvent_t ev[kMax];
+    const char* name[kMax];
+    int n = 0;
+    bool on;
+    hipStream_t s;
+    explicit StageTimer(hipStream_t st) : on(getenv("RADIUS_PBC_PROFILE") != nullptr), s(st) {}
+    // marks the end of stage `what` (the first mark opens the clock)
+    void mark(const char* what)
+    {
+        if (!on || n >= kMax) return;
+        if (hipEventCreate(&ev[n]) != hipSuccess) { on = false; return; }
+        hipEventRecord(ev[n], s);
+        name[n++] = what;
+    }
+    void report(const char* call, const Plan& p, int64_t capacity)
+    {
+        if (!on || n < 2) { release(); return; }
+        hipEventSynchronize(ev[n - 1]);
+        float total = 0;
+        fprintf(stderr, "[radius_graph_pbc profile] %s: N=%lld targets=%lld bins=%dx%dx%d tiles=%lld "
+                        "(%dx%dx%d bins) K=%d%s", call, (long long)p.n, (long long)p.nt, p.nb[0], p.nb[1],
+                p.nb[2], (long long)p.ntiles, p.T[0], p.T[1], p.T[2], p.K, p.brute ? " all-pairs" : "");
+        if (capacity >= 0) fprintf(stderr, " edge capacity=%lld", (long long)capacity);
+        fprintf(stderr, "\n");
+        for (int i = 1; i < n; ++i) {
+            float ms = 0;
+            hipEventElapsedTime(&ms, ev[i - 1], ev[i]);
+            total += ms;
+            fprintf(stderr, "  %-22s %8.3f ms\n", name[i], ms);
+        }
+        fprintf(stderr, "  %-22s %8.3f ms\n", "total", total);
+        release();
+    }
+    void release()
+    {
+        for (int i = 0; i < n; ++i) hipEventDestroy(ev[i]);
+        n = 0;
+    }
+    ~StageTimer() { release(); }
+};
+
 // Validates the description and builds the plan (host only).
 dg_status make_plan(const dg_graph_desc* d, Plan& p)
 {
@@ -1984,15 +2031,22 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
                                 at<int64_t>(ws, p.o_part), s, totals);
         return check_launch("dg_graph_count(brute)");
     }
+    StageTimer clk(s);
+    clk.mark("start");
     launch_sort(p, pos, target_idx, ws, totals, s);
+    clk.mark("sfc reorder + sort");
     // 6. degrees
     SearchArgs a = search_args(p, pos, ws);
     a.counts_user = counts_out;
     launch_count_kernel(a, (unsigned)p.ntiles, s);
+    clk.mark("count");
     // 7. tile offsets in output order, and the total
     excl_scan<int, int64_t>(at<int>(ws, p.o_ttot), p.ntiles, at<int64_t>(ws, p.o_tbase),
                             at<int64_t>(ws, p.o_part), s, totals);
-    return check_launch("dg_graph_count");
+    clk.mark("tile offset scan");
+    st = check_launch("dg_graph_count");
+    clk.report("dg_graph_count", p, -1);
+    return st;
 }
 
 dg_status dg_graph_read_totals(const dg_graph_desc* desc, const void* ws, int64_t* total_edges,
@@ -2053,9 +2107,15 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
     a.out_src = edge_src; a.out_dst = edge_dst; a.out_shift = cell_shift;
     a.out_vec = edge_vec; a.out_dist = edge_dist; a.vout_f64 = vec_dtype == DG_F64;
     a.capacity = capacity;
+    StageTimer clk(s);
+    clk.mark("start");
     hipLaunchKernelGGL(expand_kernel, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    clk.mark("write (slot expansion)");
     hipLaunchKernelGGL(search_kernel<1>, dim3((unsigned)std::min<int64_t>(p.ntiles, kFixGrid)), dim3(kBlock), 0, s, a);
-    return check_launch("dg_graph_write");
+    clk.mark("write (fix-up)");
+    st = check_launch("dg_graph_write");
+    clk.report("dg_graph_write", p, capacity);
+    return st;
 }
 
 dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,

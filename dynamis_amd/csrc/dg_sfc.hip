@@ -268,6 +268,7 @@ __device__ __forceinline__ double shift_at(const void* sh, int dt, int64_t k)
 {
     if (dt == DG_F32) return (double)((const float*)sh)[k];
     if (dt == DG_F64) return ((const double*)sh)[k];
+    if (dt == DG_I32) return (double)((const int32_t*)sh)[k];
     return (double)((const int64_t*)sh)[k];
 }
 
@@ -275,11 +276,17 @@ struct FilterCell {
     double c[9];
 };
 
-// keep iff canonical d2 <= r^2 (dist_graph_ops_kernels.cu:16-43 keeps d2 <= r2, no lower bound)
-__device__ __forceinline__ bool filter_keep(const void* __restrict__ pos, int f64, const FilterCell& C,
-                                            double r2, int64_t s, int64_t d, const void* __restrict__ sh,
-                                            int sdt, int64_t e)
+// keep iff canonical d2 <= r^2 (dist_graph_ops_kernels.cu:16-43 keeps d2 <= r2, no lower bound).
+// An edge naming an atom outside [0, n) is dropped, and raises *bad when bad is given.
+__device__ __forceinline__ bool filter_keep(const void* __restrict__ pos, int f64, int64_t n,
+                                            const FilterCell& C, double r2, int64_t s, int64_t d,
+                                            const void* __restrict__ sh, int sdt, int64_t e,
+                                            int* __restrict__ bad)
 {
+    if ((uint64_t)s >= (uint64_t)n || (uint64_t)d >= (uint64_t)n) {
+        if (bad) atomicOr(bad, 1);
+        return false;
+    }
     double ps[3], pt[3];
     if (f64) {
         const double* a = (const double*)pos;
@@ -297,14 +304,25 @@ __device__ __forceinline__ bool filter_keep(const void* __restrict__ pos, int f6
     return d2 <= r2;
 }
 
-__global__ void filter_flag_kernel(const void* __restrict__ pos, int f64, FilterCell C, double r2,
-                                   const int64_t* __restrict__ src, const int64_t* __restrict__ dst,
-                                   const void* __restrict__ sh, int sdt, int64_t E,
-                                   int* __restrict__ flag)
+__global__ void filter_flag_kernel(const void* __restrict__ pos, int f64, int64_t n, FilterCell C,
+                                   double r2, const int64_t* __restrict__ src,
+                                   const int64_t* __restrict__ dst, const void* __restrict__ sh,
+                                   int sdt, int64_t E, int* __restrict__ flag, int* __restrict__ bad)
 {
     int64_t e = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (e >= E) return;
-    flag[e] = filter_keep(pos, f64, C, r2, src[e], dst[e], sh, sdt, e) ? 1 : 0;
+    flag[e] = filter_keep(pos, f64, n, C, r2, src[e], dst[e], sh, sdt, e, bad) ? 1 : 0;
+}
+
+__global__ void filter_clear_kernel(int* __restrict__ bad)
+{
+    if (threadIdx.x == 0) *bad = 0;
+}
+
+// n_kept = -1 when an edge named an atom outside [0, n)
+__global__ void filter_bad_kernel(const int* __restrict__ bad, int64_t* __restrict__ n_kept)
+{
+    if (threadIdx.x == 0 && *bad) *n_kept = -1;
 }
 
 // Two-pass compaction (count, then write in order): a workgroup of 256 threads takes
@@ -316,10 +334,10 @@ __global__ void filter_flag_kernel(const void* __restrict__ pos, int f64, Filter
 constexpr int kFilterPer = 1;
 constexpr int kFilterTile = 256 * kFilterPer;
 
-__device__ __forceinline__ int filter_tile_flags(const void* pos, int f64, const FilterCell& C,
-                                                 double r2, const int64_t* src, const int64_t* dst,
-                                                 const void* sh, int sdt, int64_t E, int64_t e0,
-                                                 int64_t* s, int64_t* d, bool* keep)
+__device__ __forceinline__ int filter_tile_flags(const void* pos, int f64, int64_t na,
+                                                 const FilterCell& C, double r2, const int64_t* src,
+                                                 const int64_t* dst, const void* sh, int sdt, int64_t E,
+                                                 int64_t e0, int64_t* s, int64_t* d, bool* keep, int* bad)
 {
     int n = 0;
 #pragma unroll
@@ -329,7 +347,7 @@ __device__ __forceinline__ int filter_tile_flags(const void* pos, int f64, const
         if (e < E) {
             s[k] = src[e];
             d[k] = dst[e];
-            keep[k] = filter_keep(pos, f64, C, r2, s[k], d[k], sh, sdt, e);
+            keep[k] = filter_keep(pos, f64, na, C, r2, s[k], d[k], sh, sdt, e, bad);
         }
         n += keep[k] ? 1 : 0;
     }
@@ -337,17 +355,18 @@ __device__ __forceinline__ int filter_tile_flags(const void* pos, int f64, const
 }
 
 __global__ __launch_bounds__(256) void filter_count_kernel(const void* __restrict__ pos, int f64,
-                                                           FilterCell C, double r2,
+                                                           int64_t na, FilterCell C, double r2,
                                                            const int64_t* __restrict__ src,
                                                            const int64_t* __restrict__ dst,
                                                            const void* __restrict__ sh, int sdt,
-                                                           int64_t E, int* __restrict__ bcnt)
+                                                           int64_t E, int* __restrict__ bcnt,
+                                                           int* __restrict__ bad)
 {
     __shared__ int s_w[4];
     const int64_t e0 = (int64_t)blockIdx.x * kFilterTile + (int64_t)threadIdx.x * kFilterPer;
     int64_t s[kFilterPer], d[kFilterPer];
     bool keep[kFilterPer];
-    const int n = filter_tile_flags(pos, f64, C, r2, src, dst, sh, sdt, E, e0, s, d, keep);
+    const int n = filter_tile_flags(pos, f64, na, C, r2, src, dst, sh, sdt, E, e0, s, d, keep, bad);
     int tot;
     block_excl_scan<int, 256>(n, s_w, &tot);
     if (threadIdx.x == 0) bcnt[blockIdx.x] = tot;
@@ -355,7 +374,7 @@ __global__ __launch_bounds__(256) void filter_count_kernel(const void* __restric
 
 template <typename ST>
 __global__ __launch_bounds__(256) void filter_write_kernel(const void* __restrict__ pos, int f64,
-                                                           FilterCell C, double r2,
+                                                           int64_t na, FilterCell C, double r2,
                                                            const int64_t* __restrict__ src,
                                                            const int64_t* __restrict__ dst,
                                                            const ST* __restrict__ sh, int sdt,
@@ -368,7 +387,7 @@ __global__ __launch_bounds__(256) void filter_write_kernel(const void* __restric
     const int64_t e0 = (int64_t)blockIdx.x * kFilterTile + (int64_t)threadIdx.x * kFilterPer;
     int64_t s[kFilterPer], d[kFilterPer];
     bool keep[kFilterPer];
-    const int n = filter_tile_flags(pos, f64, C, r2, src, dst, sh, sdt, E, e0, s, d, keep);
+    const int n = filter_tile_flags(pos, f64, na, C, r2, src, dst, sh, sdt, E, e0, s, d, keep, nullptr);
     int tot;
     int64_t o = boff[blockIdx.x] + block_excl_scan<int, 256>(n, s_w, &tot);
 #pragma unroll
@@ -433,7 +452,7 @@ dg_status filter_check(int32_t pos_dtype, int32_t shift_dtype, double radius, in
                        int64_t n_atoms)
 {
     if (pos_dtype != DG_F32 && pos_dtype != DG_F64) return fail(DG_ERR_INVALID, "pos dtype");
-    if (shift_dtype != DG_F32 && shift_dtype != DG_F64 && shift_dtype != DG_I64)
+    if (shift_dtype != DG_F32 && shift_dtype != DG_F64 && shift_dtype != DG_I64 && shift_dtype != DG_I32)
         return fail(DG_ERR_INVALID, "shift dtype");
     if (!(radius > 0.0)) return fail(DG_ERR_INVALID, "radius must be positive");
     if (E < 0 || n_atoms < 0) return fail(DG_ERR_INVALID, "negative size");
@@ -545,7 +564,7 @@ dg_status dg_sfc_labels(const int64_t* perm, int64_t n, int64_t W, const int64_t
 size_t dg_filter_workspace_size(int64_t E)
 {
     if (E < 0) return 0;
-    return al(4 * (size_t)E) + al(8 * (size_t)(E + 1)) + al(8 * ((size_t)E / kScanTile + 2));
+    return al(4 * (size_t)E) + al(8 * (size_t)(E + 1)) + al(8 * ((size_t)E / kScanTile + 2)) + al(8);
 }
 
 dg_status dg_filter_edges_to_radius(const void* pos, int32_t pos_dtype, int64_t n_atoms,
@@ -554,31 +573,49 @@ dg_status dg_filter_edges_to_radius(const void* pos, int32_t pos_dtype, int64_t 
                                     int64_t E, int64_t* keep_idx, int64_t* n_kept, void* ws,
                                     size_t ws_bytes, hipStream_t s)
 {
-    if (pos_dtype != DG_F32 && pos_dtype != DG_F64) return fail(DG_ERR_INVALID, "pos dtype");
-    if (shift_dtype != DG_F32 && shift_dtype != DG_F64 && shift_dtype != 2)
-        return fail(DG_ERR_INVALID, "shift dtype");
-    if (!(radius > 0.0)) return fail(DG_ERR_INVALID, "radius must be positive");
-    if (E < 0 || n_atoms < 0) return fail(DG_ERR_INVALID, "negative size");
+    dg_status st = filter_check(pos_dtype, shift_dtype, radius, E, n_atoms);
+    if (st != DG_OK) return st;
     if (ws_bytes < dg_filter_workspace_size(E)) return fail(DG_ERR_WORKSPACE, "workspace too small");
     char* w = (char*)ws;
     int* flag = (int*)w;
     int64_t* pre = (int64_t*)(w + al(4 * (size_t)E));
     int64_t* part = (int64_t*)(w + al(4 * (size_t)E) + al(8 * (size_t)(E + 1)));
+    int* bad = (int*)(w + al(4 * (size_t)E) + al(8 * (size_t)(E + 1)) + al(8 * ((size_t)E / kScanTile + 2)));
+    hipLaunchKernelGGL(filter_clear_kernel, dim3(1), dim3(64), 0, s, bad);
     if (E > 0)
         hipLaunchKernelGGL(filter_flag_kernel, dim3(nblk(E)), dim3(256), 0, s, pos,
-                           (int)(pos_dtype == DG_F64), filter_cell(cell), radius * radius, src, dst,
-                           shift, (int)shift_dtype, E, flag);
+                           (int)(pos_dtype == DG_F64), n_atoms, filter_cell(cell), radius * radius, src,
+                           dst, shift, (int)shift_dtype, E, flag, bad);
     device_excl_scan<int, int64_t>(flag, E, pre, part, s);
     hipLaunchKernelGGL(filter_compact_kernel, dim3(E > 0 ? nblk(E) : 1), dim3(256), 0, s,
                        (const int*)flag, (const int64_t*)pre, E, keep_idx, n_kept);
+    hipLaunchKernelGGL(filter_bad_kernel, dim3(1), dim3(64), 0, s, (const int*)bad, n_kept);
     return launch_ok("dg_filter_edges_to_radius");
+}
+
+// Workspace of the count / write pair: per-block kept counts (nb + 1), their offsets
+// (nb + 1), scan partials, and the out-of-range flag.
+struct Filter2Layout {
+    size_t o_bcnt, o_boff, o_part, o_bad, total;
+    int64_t nb;
+};
+static Filter2Layout filter2_layout(int64_t E)
+{
+    Filter2Layout L;
+    L.nb = (E + kFilterTile - 1) / kFilterTile;
+    const size_t nb = (size_t)L.nb;
+    L.o_bcnt = 0;
+    L.o_boff = al(4 * (nb + 1));
+    L.o_part = L.o_boff + al(8 * (nb + 1));
+    L.o_bad = L.o_part + al(8 * (nb / kScanTile + 2));
+    L.total = L.o_bad + al(8);
+    return L;
 }
 
 size_t dg_filter2_workspace_size(int64_t E)
 {
     if (E < 0) return 0;
-    const size_t nb = (size_t)((E + kFilterTile - 1) / kFilterTile);
-    return al(4 * (nb + 1)) + al(8 * (nb + 1)) + al(8 * (nb / kScanTile + 2));
+    return filter2_layout(E).total;
 }
 
 dg_status dg_filter_count(const void* pos, int32_t pos_dtype, int64_t n_atoms, const double* cell,
@@ -588,17 +625,21 @@ dg_status dg_filter_count(const void* pos, int32_t pos_dtype, int64_t n_atoms, c
 {
     dg_status st = filter_check(pos_dtype, shift_dtype, radius, E, n_atoms);
     if (st != DG_OK) return st;
-    if (ws_bytes < dg_filter2_workspace_size(E)) return fail(DG_ERR_WORKSPACE, "workspace too small");
-    const int64_t nb = (E + kFilterTile - 1) / kFilterTile;
+    const Filter2Layout FL = filter2_layout(E);
+    if (ws_bytes < FL.total) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    const int64_t nb = FL.nb;
     char* w = (char*)ws;
-    int* bcnt = (int*)w;
-    int64_t* boff = (int64_t*)(w + al(4 * (size_t)(nb + 1)));
-    int64_t* part = (int64_t*)(w + al(4 * (size_t)(nb + 1)) + al(8 * (size_t)(nb + 1)));
+    int* bcnt = (int*)(w + FL.o_bcnt);
+    int64_t* boff = (int64_t*)(w + FL.o_boff);
+    int64_t* part = (int64_t*)(w + FL.o_part);
+    int* bad = (int*)(w + FL.o_bad);
+    hipLaunchKernelGGL(filter_clear_kernel, dim3(1), dim3(64), 0, s, bad);
     if (nb > 0)
         hipLaunchKernelGGL(filter_count_kernel, dim3((unsigned)nb), dim3(256), 0, s, pos,
-                           (int)(pos_dtype == DG_F64), filter_cell(cell), radius * radius, src, dst,
-                           shift, (int)shift_dtype, E, bcnt);
+                           (int)(pos_dtype == DG_F64), n_atoms, filter_cell(cell), radius * radius, src,
+                           dst, shift, (int)shift_dtype, E, bcnt, bad);
     excl_scan<int, int64_t>(bcnt, nb, boff, part, s, n_kept);
+    hipLaunchKernelGGL(filter_bad_kernel, dim3(1), dim3(64), 0, s, (const int*)bad, n_kept);
     return launch_ok("dg_filter_count");
 }
 
@@ -609,25 +650,30 @@ dg_status dg_filter_write(const void* pos, int32_t pos_dtype, int64_t n_atoms, c
 {
     dg_status st = filter_check(pos_dtype, shift_dtype, radius, E, n_atoms);
     if (st != DG_OK) return st;
-    if (ws_bytes < dg_filter2_workspace_size(E)) return fail(DG_ERR_WORKSPACE, "workspace too small");
-    const int64_t nb = (E + kFilterTile - 1) / kFilterTile;
+    const Filter2Layout FL = filter2_layout(E);
+    if (ws_bytes < FL.total) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    const int64_t nb = FL.nb;
     if (nb == 0) return DG_OK;
-    const int64_t* boff = (const int64_t*)((const char*)ws + al(4 * (size_t)(nb + 1)));
+    const int64_t* boff = (const int64_t*)((const char*)ws + FL.o_boff);
     const int f64 = (int)(pos_dtype == DG_F64);
     const FilterCell C = filter_cell(cell);
     const double r2 = radius * radius;
     if (shift_dtype == DG_F32)
-        hipLaunchKernelGGL(filter_write_kernel<float>, dim3((unsigned)nb), dim3(256), 0, s, pos, f64, C,
-                           r2, src, dst, (const float*)shift, (int)shift_dtype, E, boff, out_src,
-                           out_dst, (float*)out_shift);
+        hipLaunchKernelGGL(filter_write_kernel<float>, dim3((unsigned)nb), dim3(256), 0, s, pos, f64,
+                           n_atoms, C, r2, src, dst, (const float*)shift, (int)shift_dtype, E, boff,
+                           out_src, out_dst, (float*)out_shift);
     else if (shift_dtype == DG_F64)
-        hipLaunchKernelGGL(filter_write_kernel<double>, dim3((unsigned)nb), dim3(256), 0, s, pos, f64, C,
-                           r2, src, dst, (const double*)shift, (int)shift_dtype, E, boff, out_src,
-                           out_dst, (double*)out_shift);
+        hipLaunchKernelGGL(filter_write_kernel<double>, dim3((unsigned)nb), dim3(256), 0, s, pos, f64,
+                           n_atoms, C, r2, src, dst, (const double*)shift, (int)shift_dtype, E, boff,
+                           out_src, out_dst, (double*)out_shift);
+    else if (shift_dtype == DG_I32)
+        hipLaunchKernelGGL(filter_write_kernel<int32_t>, dim3((unsigned)nb), dim3(256), 0, s, pos, f64,
+                           n_atoms, C, r2, src, dst, (const int32_t*)shift, (int)shift_dtype, E, boff,
+                           out_src, out_dst, (int32_t*)out_shift);
     else
         hipLaunchKernelGGL(filter_write_kernel<int64_t>, dim3((unsigned)nb), dim3(256), 0, s, pos, f64,
-                           C, r2, src, dst, (const int64_t*)shift, (int)shift_dtype, E, boff, out_src,
-                           out_dst, (int64_t*)out_shift);
+                           n_atoms, C, r2, src, dst, (const int64_t*)shift, (int)shift_dtype, E, boff,
+                           out_src, out_dst, (int64_t*)out_shift);
     return launch_ok("dg_filter_write");
 }
 

@@ -181,10 +181,11 @@ def radius_graph_pbc_vectors(pos, cell, pbc, radius, target_indices=None, vector
     and distances |v| (fp64 exact, or fp32 correctly rounded from fp64).
 
     Returns (edge_index, cell_shifts, num_neighbors_image, neighbor_counts, edge_vec,
-    edge_dist).  radius is used as given (not rounded to fp32).
+    edge_dist).  radius is rounded to fp32, as every other entry point does, so the edge
+    set is the one radius_graph_pbc_ex returns at the same radius.
     """
     pos, cell, pbc, ti = _validate(pos, cell, pbc, radius, None, target_indices)
-    return build_graph(pos, cell, pbc, float(radius), ti, return_vectors=True,
+    return build_graph(pos, cell, pbc, _r32(radius), ti, return_vectors=True,
                        vector_dtype=vector_dtype)
 
 
@@ -219,10 +220,18 @@ def filter_edges_to_radius(edges, cell_shifts, pos, cell, radius):
     edges = edges.contiguous()
     pos = pos.contiguous()
     sh = cell_shifts.contiguous()
-    if sh.dtype == torch.float32:
+    # The kernels read float32, float64, int32 and int64 shifts.  Other dtypes go through
+    # one whose values hold theirs exactly (float16 / bfloat16 -> float32, other integer
+    # types -> int64) and come back unchanged, so the returned shifts are bit-equal to the
+    # input rows, as the reference's compaction of the original tensor gives
+    # (dist_graph_ops_kernels.cu:95-100).
+    native = {torch.float32: L.DG_F32, torch.float64: L.DG_F64, torch.int64: L.DG_I64,
+              torch.int32: L.DG_I32}
+    if sh.dtype in native:
+        sdt = native[sh.dtype]
+    elif sh.is_floating_point():
+        sh = sh.to(torch.float32)
         sdt = L.DG_F32
-    elif sh.dtype == torch.float64:
-        sdt = L.DG_F64
     else:
         sh = sh.to(torch.int64)
         sdt = L.DG_I64
@@ -241,6 +250,7 @@ def filter_edges_to_radius(edges, cell_shifts, pos, cell, radius):
         # exact-size allocation): the kept edges, in order, straight into the outputs
         L.check(lib.dg_filter_count(*args, L.ptr(nk), L.ptr(ws), wsb, s), "filter_edges_to_radius")
         k = int(nk.item())
+        _check(k >= 0, f"filter_edges_to_radius: edges hold atom indices outside [0, {pos.size(0)})")
         out_e = torch.empty((2, k), dtype=torch.int64, device=dev)
         out_s = torch.empty((k, 3), dtype=sh.dtype, device=dev)
         if k > 0:

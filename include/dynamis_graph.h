@@ -137,9 +137,11 @@ dg_status dg_graph_build_noalloc(const dg_graph_desc* desc, const void* pos,
 /* Order-preserving filter of an edge list to radius (keep iff d2 <= radius^2, canonical
  * fp64 d2).  Replaces filter_edges_to_radius (dist_graph_ops.cpp:5-35,
  * dist_graph_ops_kernels.cu:16-43,62-102).
- *   edge_src/edge_dst int64 [n_edges], cell_shift [n_edges,3] of shift_dtype
+ *   edge_src/edge_dst int64 [n_edges], cell_shift [n_edges,3] of shift_dtype (DG_F32,
+ *     DG_F64, DG_I64 or DG_I32)
  *   keep_idx out int64 [n_edges]: indices of kept edges, ascending
- *   n_kept   out int64 (device, one value)
+ *   n_kept   out int64 (device, one value); -1 if an edge names an atom outside
+ *            [0, n_atoms) (such edges are never read through: no position is gathered)
  *   workspace of dg_filter_workspace_size(n_edges) bytes */
 size_t dg_filter_workspace_size(int64_t n_edges);
 dg_status dg_filter_edges_to_radius(const void* pos, int32_t pos_dtype, int64_t n_atoms,
@@ -152,7 +154,8 @@ dg_status dg_filter_edges_to_radius(const void* pos, int32_t pos_dtype, int64_t 
 /* The same filter as a count / write pair that writes the kept edges themselves (in order,
  * shifts in shift_dtype), for exact-size outputs without an index gather: the form the
  * Python filter_edges_to_radius uses.  Replaces the same reference function as above.
- *   dg_filter_count: n_kept out int64 (device, one value); workspace of
+ *   dg_filter_count: n_kept out int64 (device, one value; -1 if an edge names an atom
+ *     outside [0, n_atoms)); workspace of
  *     dg_filter2_workspace_size(n_edges) bytes, kept for dg_filter_write
  *   dg_filter_write: out_src/out_dst int64 [n_kept], out_shift [n_kept,3] of shift_dtype;
  *     same inputs and workspace as the dg_filter_count call before it */

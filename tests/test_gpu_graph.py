@@ -292,23 +292,107 @@ def test_edge_vectors(cuda, which):
             assert np.all(np.abs(got[4].astype(np.float64) - want[4]) <= 2 * ulp)
 
 
-def test_filter_edges_to_radius(cuda):
-    box = configs.uniform(8000, seed=17, dtype=np.float32)
+def _filter_case(cuda, n, seed, r_big, r, dtype):
+    box = configs.uniform(n, seed=seed, dtype=np.float32)
     p = torch.from_numpy(box.pos).to(cuda)
     c = torch.from_numpy(box.cell)
     b = torch.tensor([True] * 3)
-    ei, co, _ = impl.radius_graph_pbc(p, c, b, 6.5, 0, False)
-    ef, cf = impl.filter_edges_to_radius(ei, co, p, c, 6.0)
-    e6, c6, _ = impl.radius_graph_pbc(p, c, b, 6.0, 0, False)
-    got = oracle.canonical_sort(ef[0].cpu().numpy(), ef[1].cpu().numpy(), cf.cpu().numpy().astype(np.int64))
+    ei, co, _ = impl.radius_graph_pbc(p, c, b, r_big, 0, False)
+    sh = co.to(dtype)
+    ef, cf = impl.filter_edges_to_radius(ei, sh, p, c, r)
+    e6, c6, _ = impl.radius_graph_pbc(p, c, b, r, 0, False)
+    got = oracle.canonical_sort(ef[0].cpu().numpy(), ef[1].cpu().numpy(), cf.float().cpu().numpy().astype(np.int64))
     want = oracle.canonical_sort(e6[0].cpu().numpy(), e6[1].cpu().numpy(), c6.cpu().numpy().astype(np.int64))
     for a, bb in zip(got, want):
         assert np.array_equal(a, bb)
-    # order preserving: kept edges appear in their original relative order
-    keep = oracle.filter_edges(box.pos, box.cell, 6.0, ei[0].cpu().numpy(), ei[1].cpu().numpy(),
+    # order preserving: kept edges appear in their original relative order, and the kept
+    # shifts are the input rows bit for bit, in the input dtype
+    keep = oracle.filter_edges(box.pos, box.cell, r, ei[0].cpu().numpy(), ei[1].cpu().numpy(),
                                co.cpu().numpy().astype(np.int32))
+    kt = torch.from_numpy(np.nonzero(keep)[0]).to(cuda)
     assert np.array_equal(ef.cpu().numpy(), ei.cpu().numpy()[:, keep])
-    assert cf.dtype == co.dtype
+    assert cf.dtype == sh.dtype and torch.equal(cf, sh.index_select(0, kt))
+    return ei.shape[1]
+
+
+@pytest.mark.parametrize("dtype", [torch.float32, torch.float64, torch.int64, torch.int32,
+                                   torch.float16, torch.bfloat16])
+def test_filter_edges_to_radius(cuda, dtype):
+    _announce(f"filter, shifts {dtype}")
+    _filter_case(cuda, 8000, 17, 6.5, 6.0, dtype)
+
+
+def test_filter_large_list(cuda):
+    """More than 2.1M edges: the per-block kept counts (one per 256 edges) exceed one
+    workgroup's scan, so the multi-kernel device scan produces the block offsets; the last
+    block is partial."""
+    _announce("filter, large list")
+    E = _filter_case(cuda, 30000, 18, 6.5, 6.0, torch.float32)
+    assert E > 2_100_000 and E % 256 != 0
+
+
+def test_filter_rejects_out_of_range_atoms(cuda):
+    _announce("filter, out-of-range atom index")
+    box = configs.uniform(2000, seed=19, dtype=np.float32)
+    p = torch.from_numpy(box.pos).to(cuda)
+    c = torch.from_numpy(box.cell)
+    ei, co, _ = impl.radius_graph_pbc(p, c, torch.tensor([True] * 3), 6.0, 0, False)
+    for bad in (2000, -1):
+        e2 = ei.clone()
+        e2[0, 17] = bad
+        with pytest.raises(RuntimeError, match="outside"):
+            impl.filter_edges_to_radius(e2, co, p, c, 5.0)
+
+
+def test_vectors_round_radius_like_the_build(cuda):
+    """radius_graph_pbc_vectors rounds the radius to fp32 as radius_graph_pbc_ex does, so
+    both return the same edge set at a radius fp32 cannot hold exactly."""
+    _announce("vectors radius rounding")
+    box = configs.uniform(20000, seed=23, dtype=np.float32)
+    p = torch.from_numpy(box.pos).to(cuda)
+    c = torch.from_numpy(box.cell)
+    b = torch.tensor([True] * 3)
+    r = 5.3
+    assert float(np.float32(r)) != r
+    e1, s1, _, n1 = impl.radius_graph_pbc_ex(p, c, b, r, 0, False)
+    e2, s2, _, n2, vec, dist = impl.radius_graph_pbc_vectors(p, c, b, r)
+    assert torch.equal(e1, e2) and torch.equal(s1, s2) and torch.equal(n1, n2)
+    assert float(dist.max()) <= float(np.float32(r))
+
+
+def test_far_atom_is_rejected(cuda):
+    """An atom more than 255 cell lengths outside the cell (along a lattice vector) is
+    refused with an error naming the limit; 250 cell lengths are accepted."""
+    _announce("far atom")
+    box = configs.uniform(500, seed=24, dtype=np.float64, radius=5.0)
+    c = torch.from_numpy(box.cell)
+    b = torch.tensor([True] * 3)
+    L = float(box.cell[0, 0])
+    pos = box.pos.copy()
+    pos[7, 1] += 250.0 * L
+    check_parity(pos, box.cell, box.pbc, 5.0, cuda, name="250 cells out")
+    pos[7, 1] += 10.0 * L
+    with pytest.raises(RuntimeError, match="255 cell lengths"):
+        impl.radius_graph_pbc(torch.from_numpy(pos).to(cuda), c, b, 5.0, 0, False)
+
+
+def test_stage_timer(cuda, capfd, monkeypatch):
+    """RADIUS_PBC_PROFILE (as the reference's radius_graph_kernels.cu:444-465) prints the
+    time of every stage of a build to stderr; unset, nothing is printed."""
+    _announce("stage timer")
+    box = configs.uniform(20000, seed=25, dtype=np.float32)
+    p = torch.from_numpy(box.pos).to(cuda)
+    c = torch.from_numpy(box.cell)
+    b = torch.tensor([True] * 3)
+    impl.radius_graph_pbc(p, c, b, 6.0, 0, False)
+    torch.cuda.synchronize()
+    assert "[radius_graph_pbc profile]" not in capfd.readouterr().err
+    monkeypatch.setenv("RADIUS_PBC_PROFILE", "1")
+    impl.radius_graph_pbc(p, c, b, 6.0, 0, False)
+    err = capfd.readouterr().err
+    for stage in ("dg_graph_count", "sfc reorder + sort", "count", "dg_graph_write",
+                  "write (slot expansion)", "write (fix-up)", "total"):
+        assert stage in err, err
 
 
 # ---- prefilter band: pairs within a few ulp of the cutoff ---------------------------
