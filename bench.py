@@ -15,6 +15,7 @@ from __future__ import annotations
 
 import argparse
 import ctypes
+import itertools
 import json
 import os
 import sys
@@ -75,7 +76,7 @@ def main():
         return bench_halo(args)
 
     box = {"C1": configs.fcc, "C2": configs.c2, "C3": configs.c3, "C4": configs.c4,
-           "C5": configs.c5}[args.config]()
+           "C4-500k": lambda: configs.c4(scale=1.3934), "C5": configs.c5}[args.config]()
     dev = torch.device("cuda:0")
     torch.cuda.set_device(dev)
     lib = L.lib()
@@ -112,10 +113,7 @@ def main():
     nframes = args.trajectory if args.trajectory >= 0 else (100 if args.config == "C5" else 0)
     frames = [pos]
     if nframes > 1:
-        g = torch.Generator(device=dev).manual_seed(7)
-        for _ in range(nframes - 1):
-            frames.append(frames[-1] + args.sigma * torch.randn(pos.shape, generator=g, device=dev,
-                                                                dtype=pos.dtype))
+        frames = list(itertools.islice(configs.walk(pos, args.sigma, seed=7), nframes))
     torch.cuda.synchronize()
 
     def step(ev=None, k=0):

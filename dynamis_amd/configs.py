@@ -97,3 +97,17 @@ def c5(n_owned=4_000_000, side=342.0, shell=6.0, density=0.1, seed=4, dtype=np.f
 def displace(pos, sigma, seed):
     rng = np.random.default_rng(seed)
     return (pos.astype(np.float64) + rng.normal(0.0, sigma, pos.shape)).astype(pos.dtype)
+
+
+def walk(pos, sigma, seed=7):
+    """Position frames of a random walk on the device: frame 0 is ``pos`` (a torch tensor),
+    frame k is frame k - 1 displaced by Gaussian ``sigma`` per coordinate (torch generator
+    on pos's device, seeded).  The trajectory the benchmark rebuilds from (C5: 100 frames
+    at 0.01 A)."""
+    import torch
+
+    g = torch.Generator(device=pos.device).manual_seed(seed)
+    cur = pos
+    while True:
+        yield cur
+        cur = cur + sigma * torch.randn(pos.shape, generator=g, device=pos.device, dtype=pos.dtype)
