@@ -67,6 +67,8 @@ def lib():
         L.orc_edge_vectors.argtypes = [_p, ctypes.c_int, _p, _i64, _p, _p, _p, _p, _p]
         L.orc_filter_edges.restype = _i64
         L.orc_filter_edges.argtypes = [_p, ctypes.c_int, _p, _dbl, _i64, _p, _p, _p, _p]
+        L.orc_ref32_decide.restype = None
+        L.orc_ref32_decide.argtypes = [_p, _i64, _p, _p, _dbl, _i64, _p, _p, _p, _p]
         L.orc_sfc_bounds.argtypes = [_p, _i64, _p, _p]
         L.orc_morton_keys.argtypes = [_p, _i64, _p, _p, _p]
         L.orc_hilbert_keys.argtypes = [_p, _i64, _p, _p, _p]
@@ -177,6 +179,45 @@ def filter_edges(pos, cell, radius, src, dst, shift):
     L.orc_filter_edges(_ptr(pos), int(pos.dtype == np.float64), _ptr(cell), float(radius), E,
                        _ptr(src), _ptr(dst), _ptr(shift), _ptr(keep))
     return keep.astype(bool)
+
+
+def ref32_decide(pos, cell, pbc, radius, src, dst, shift):
+    """The reference's fp32 decision (radius_graph_kernels.cu:70-141, 247-250, 515-605)
+    for candidate edges (src, dst, S): keep[e] is True iff its arithmetic emits edge e.
+    For the fp32-vs-canonical disagreement report (see graph_oracle.c)."""
+    L = lib()
+    pos = np.ascontiguousarray(pos, np.float32)
+    cell = np.ascontiguousarray(np.asarray(cell, dtype=np.float64).reshape(3, 3))
+    pbc = np.ascontiguousarray(np.asarray(pbc, dtype=np.uint8).reshape(3))
+    src = np.ascontiguousarray(src, np.int64)
+    dst = np.ascontiguousarray(dst, np.int64)
+    shift = np.ascontiguousarray(shift, np.int32)
+    keep = np.zeros(src.shape[0], np.uint8)
+    L.orc_ref32_decide(_ptr(pos), pos.shape[0], _ptr(cell), _ptr(pbc), float(radius), src.shape[0],
+                       _ptr(src), _ptr(dst), _ptr(shift), _ptr(keep))
+    return keep.astype(bool)
+
+
+def fp32_disagreement(pos, cell, pbc, radius, delta=1e-3):
+    """Canonical (fp64) edge set vs the reference's fp32 decisions on the same input.
+
+    Candidates are the canonical edges at radius + delta (the fp32 errors are orders of
+    magnitude below delta, so every edge either side can emit is among them).  Returns a
+    dict: canonical edge count, the edges only the canonical set holds, the edges only the
+    fp32 arithmetic emits, and the largest |d - r| over the differing pairs.
+    """
+    r = float(np.float32(radius))
+    c = np.asarray(cell, np.float64).astype(np.float32).astype(np.float64)
+    p32 = np.ascontiguousarray(pos, np.float32)
+    o = radius_graph(p32, c, pbc, r + delta, vectors=True)
+    canon = o["d2"] <= r * r
+    ref = ref32_decide(p32, c, pbc, r, o["src"], o["dst"], o["shift"])
+    only_c = canon & ~ref
+    only_r = ref & ~canon
+    diff = only_c | only_r
+    dmax = float(np.max(np.abs(np.sqrt(o["d2"][diff]) - r))) if diff.any() else 0.0
+    return {"edges": int(canon.sum()), "canonical_only": int(only_c.sum()),
+            "fp32_only": int(only_r.sum()), "max_abs_d_minus_r": dmax}
 
 
 def sfc_bounds(pos):

@@ -415,6 +415,102 @@ int64_t orc_filter_edges(const void* pos, int f64, const double* cell, double ra
 }
 
 /* ---------------------------------------------------------------------------------- */
+/* Reference-semantics (fp32) edge decision, for the disagreement report only.           */
+/*
+ * The reference decides every edge in fp32.  This restates that arithmetic step by step
+ * for a list of candidate edges (src, dst, S), so the canonical fp64 edge set can be
+ * compared with the one the reference would emit:
+ *   geometry   radius_graph_kernels.cu:515-594 (host, fp32, no contraction): d_face,
+ *              rep = ceil(r / d_face), cutoff_frac = r / d_face, cell^-1 = adj / det
+ *   wrap       :596-605  frac = pos . cell^-1 (at::mm), floor, pos_w = pos - floor . cell
+ *   images     :70-141   s = pos_w . cell^-1; image (dx,dy,dz) kept iff, per axis, a
+ *              shift up needs s < cf, a shift down needs s > 1 - cf (non-PBC: 0 only);
+ *              image = pos_w + (dx,dy,dz) . cell
+ *   predicate  :247-250, 399-400  d = target_w - image, d2 = dx^2 + dy^2 + dz^2,
+ *              edge iff d2 <= r*r (fp32) and d2 > 1e-8f
+ *   shift      :282-303  S = (dx,dy,dz) + floor_tgt - floor_src
+ * Device expressions of the form a*b + c*d + e*f are taken as nvcc contracts them by
+ * default, fma(e, f, fma(c, d, a*b)); the two at::mm products (cuBLAS) as the same fma
+ * chain in k order.  That GEMM rounding is an assumption (the library's reduction order
+ * is not published), so single decisions that hinge on it are unpinned.
+ * keep[e] = 1 iff the reference's arithmetic emits candidate e.
+ */
+void orc_ref32_decide(const float* pos, int64_t n, const double* cell_d, const uint8_t* pbc,
+                      double radius_d, int64_t E, const int64_t* src, const int64_t* dst,
+                      const int32_t* shift, uint8_t* keep)
+{
+    float c[9];
+    for (int k = 0; k < 9; k++) c[k] = (float)cell_d[k];
+    const float radius = (float)radius_d;
+    const float *a0 = c, *a1 = c + 3, *a2 = c + 6;
+    float c12[3] = {a1[1] * a2[2] - a1[2] * a2[1], a1[2] * a2[0] - a1[0] * a2[2], a1[0] * a2[1] - a1[1] * a2[0]};
+    float vol = a0[0] * c12[0] + a0[1] * c12[1] + a0[2] * c12[2];
+    float abs_vol = fabsf(vol);
+    float c20[3] = {a2[1] * a0[2] - a2[2] * a0[1], a2[2] * a0[0] - a2[0] * a0[2], a2[0] * a0[1] - a2[1] * a0[0]};
+    float c01[3] = {a0[1] * a1[2] - a0[2] * a1[1], a0[2] * a1[0] - a0[0] * a1[2], a0[0] * a1[1] - a0[1] * a1[0]};
+    float nrm[3] = {sqrtf(c12[0] * c12[0] + c12[1] * c12[1] + c12[2] * c12[2]),
+                    sqrtf(c20[0] * c20[0] + c20[1] * c20[1] + c20[2] * c20[2]),
+                    sqrtf(c01[0] * c01[0] + c01[1] * c01[1] + c01[2] * c01[2])};
+    int rep[3];
+    float cf[3];
+    for (int d = 0; d < 3; d++) {
+        float dface = abs_vol / nrm[d];
+        rep[d] = pbc[d] ? (int)ceilf(radius / dface) : 0;
+        cf[d] = pbc[d] ? radius / dface : 0.0f;
+    }
+    float iv = 1.0f / vol;
+    float ci[9] = {(a1[1] * a2[2] - a1[2] * a2[1]) * iv, (a0[2] * a2[1] - a0[1] * a2[2]) * iv,
+                   (a0[1] * a1[2] - a0[2] * a1[1]) * iv, (a1[2] * a2[0] - a1[0] * a2[2]) * iv,
+                   (a0[0] * a2[2] - a0[2] * a2[0]) * iv, (a0[2] * a1[0] - a0[0] * a1[2]) * iv,
+                   (a1[0] * a2[1] - a1[1] * a2[0]) * iv, (a0[1] * a2[0] - a0[0] * a2[1]) * iv,
+                   (a0[0] * a1[1] - a0[1] * a1[0]) * iv};
+    const float r2 = radius * radius;
+    /* per atom: floor of frac and the wrapped position */
+    float* ff = (float*)malloc(sizeof(float) * 3 * (size_t)(n > 0 ? n : 1));
+    float* pw = (float*)malloc(sizeof(float) * 3 * (size_t)(n > 0 ? n : 1));
+#pragma omp parallel for schedule(static)
+    for (int64_t i = 0; i < n; i++) {
+        const float* p = pos + 3 * i;
+        float f[3];
+        for (int j = 0; j < 3; j++) f[j] = floorf(fmaf(p[2], ci[6 + j], fmaf(p[1], ci[3 + j], p[0] * ci[j])));
+        for (int j = 0; j < 3; j++) {
+            ff[3 * i + j] = f[j];
+            pw[3 * i + j] = p[j] - fmaf(f[2], c[6 + j], fmaf(f[1], c[3 + j], f[0] * c[j]));
+        }
+    }
+#pragma omp parallel for schedule(static)
+    for (int64_t e = 0; e < E; e++) {
+        const int64_t sI = src[e], tI = dst[e];
+        keep[e] = 0;
+        int dd[3];
+        int ok = 1;
+        for (int d = 0; d < 3; d++) {
+            dd[d] = shift[3 * e + d] - (int)ff[3 * tI + d] + (int)ff[3 * sI + d];
+            if (dd[d] < -rep[d] || dd[d] > rep[d]) ok = 0;
+        }
+        if (!ok) continue;
+        const float* q = pw + 3 * sI;
+        float sv[3];
+        for (int j = 0; j < 3; j++) sv[j] = fmaf(q[2], ci[6 + j], fmaf(q[1], ci[3 + j], q[0] * ci[j]));
+        for (int d = 0; d < 3; d++) {
+            if (!pbc[d] && dd[d] != 0) ok = 0;
+            else if (dd[d] > 0 && !(sv[d] < cf[d])) ok = 0;
+            else if (dd[d] < 0 && !(sv[d] > 1.0f - cf[d])) ok = 0;
+        }
+        if (!ok) continue;
+        float img[3];
+        for (int j = 0; j < 3; j++)
+            img[j] = q[j] + fmaf((float)dd[2], c[6 + j], fmaf((float)dd[1], c[3 + j], (float)dd[0] * c[j]));
+        const float* t = pw + 3 * tI;
+        const float dx = t[0] - img[0], dy = t[1] - img[1], dz = t[2] - img[2];
+        const float dist2 = fmaf(dz, dz, fmaf(dy, dy, dx * dx));
+        keep[e] = (dist2 <= r2) && (dist2 > 1e-8f);
+    }
+    free(ff);
+    free(pw);
+}
+
+/* ---------------------------------------------------------------------------------- */
 /* SFC keys: partition/sfc_kernels.cu:19-109 and bounds :196-198, fp32 arithmetic.      */
 
 static uint64_t spread_bits_21(uint32_t v)
