@@ -43,9 +43,10 @@ def main():
                          "HBM before the timed region); 0 = the same positions every step.  "
                          "Default: 100 for C5 (its stated 100 rebuilds at 0.01 A per step), else 0")
     ap.add_argument("--sigma", type=float, default=0.01)
-    ap.add_argument("--path", default="graph", choices=["graph", "halo"],
+    ap.add_argument("--path", default="graph", choices=["graph", "halo", "filter"],
                     help="graph: the headline full rebuild; halo: extract_halo_info of one rank "
-                         "of an 8-way SFC partition of the same box (edges at r + 0.5)")
+                         "of an 8-way SFC partition of the same box (edges at r + 0.5); filter: "
+                         "filter_edges_to_radius of the box's edges at r + 0.5 down to r")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -74,6 +75,8 @@ def main():
 
     if args.path == "halo":
         return bench_halo(args)
+    if args.path == "filter":
+        return bench_filter(args)
 
     box = {"C1": configs.fcc, "C2": configs.c2, "C3": configs.c3, "C4": configs.c4,
            "C4-500k": lambda: configs.c4(scale=1.3934), "C5": configs.c5}[args.config]()
@@ -294,6 +297,84 @@ def cpu_baseline(args, box, n, E_gpu):
     if E_cpu != E_gpu:
         cpu["edge_count_mismatch"] = [E_cpu, E_gpu]
     return cpu
+
+
+def bench_filter(args):
+    """filter_edges_to_radius of the whole box's edges at r + 0.5 down to r: one step =
+    dg_filter_compact (one pass) into preallocated outputs of the input's size (the Python
+    call adds the allocations, one host sync and the move of the target row)."""
+    import numpy as np
+    import torch
+
+    from dynamis_amd import _lib as L
+    from dynamis_amd import configs
+    from dynamis_amd.dynamis_state import dynamis_state_impl as impl
+
+    skin = 0.5
+    box = {"C2": configs.c2, "C3": configs.c3}[args.config]()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = L.lib()
+    pos = torch.from_numpy(box.pos).to(dev)
+    n = pos.shape[0]
+    cell = torch.from_numpy(np.asarray(box.cell))
+    ei, sh, _ = impl.radius_graph_pbc(pos, cell, torch.tensor(list(box.pbc)), box.radius + skin, 0, False)
+    E = ei.shape[1]
+    r = float(np.float32(box.radius))
+    cbuf = (L.ctypes.c_double * 9)(*np.asarray(box.cell, np.float64).astype(np.float32).astype(np.float64).reshape(-1).tolist())
+    wsb = lib.dg_filter_compact_workspace_size(E)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    nk = torch.empty(1, dtype=torch.int64, device=dev)
+    base = ei.data_ptr()
+    fargs = (L.ptr(pos), L.DG_F32, n, cbuf, r, L.ctypes.c_void_p(base), L.ctypes.c_void_p(base + 8 * E),
+             L.ptr(sh), L.DG_F32, E)
+    s = L.stream_of(dev)
+    stream = torch.cuda.current_stream(dev)
+    out_src = torch.empty(E, dtype=torch.int64, device=dev)
+    out_dst = torch.empty(E, dtype=torch.int64, device=dev)
+    out_s = torch.empty((E, 3), dtype=torch.float32, device=dev)
+
+    def step(ev=None):
+        if ev is not None:
+            ev[0].record(stream)
+        L.check(lib.dg_filter_compact(*fargs, L.ptr(out_src), L.ptr(out_dst), L.ptr(out_s), L.ptr(nk),
+                                      L.ptr(ws), wsb, s), "filter")
+        if ev is not None:
+            ev[1].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    K = int(nk.item())
+    evs = [[torch.cuda.Event(enable_timing=True) for _ in range(2)] for _ in range(args.steps)]
+    for k in range(args.steps):
+        step(evs[k])
+    torch.cuda.synchronize()
+    ms = float(np.mean([a.elapsed_time(b) for a, b in evs]))
+    # exact-size Python call (one host sync, allocation)
+    torch.cuda.synchronize()
+    ta = time.perf_counter()
+    for _ in range(max(3, args.steps // 4)):
+        impl.filter_edges_to_radius(ei, sh, pos, cell, r)
+    torch.cuda.synchronize()
+    api_ms = (time.perf_counter() - ta) * 1e3 / max(3, args.steps // 4)
+    # algorithmic bytes: read the edge list (28 B per edge: src, dst, fp32 shift), write the
+    # kept edges (28 B each), read the positions once
+    nbytes = 28 * E + 28 * K + 12 * n
+    ach = nbytes / (ms * 1e-3) / 1e9
+    print(json.dumps({
+        "metric": "filter_edges_to_radius edges/s (edges at r+0.5 filtered to r)",
+        "value": round(E / (ms * 1e-3) / 1e9, 3), "unit": "Gedges/s", "n_gpus": 1, "steps": args.steps,
+        "warmup": args.warmup, "ms_per_step": round(ms, 4), "higher_is_better": True,
+        "scaling": "weak", "vs_baseline": None, "dtype": "fp32 positions, fp64 predicate",
+        "data": "synthetic (seeded numpy uniform box)",
+        "config": {"workload": f"filter, {args.config} N={n}, r={box.radius}+{skin} -> {box.radius}",
+                   "edges_in": E, "edges_kept": K},
+        "api_ms": round(api_ms, 3),
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "dg_filter_compact (single pass, all kernels)",
+                     "algorithmic_bytes": nbytes}}), flush=True)
 
 
 def bench_halo(args):

@@ -82,6 +82,9 @@ def lib():
                                    _p, _sz, _p]),
         "dg_filter_write": (_i32, [_p, _i32, _i64, _p, ctypes.c_double, _p, _p, _p, _i32, _i64, _p,
                                    _sz, _p, _p, _p, _p]),
+        "dg_filter_compact_workspace_size": (_sz, [_i64]),
+        "dg_filter_compact": (_i32, [_p, _i32, _i64, _p, ctypes.c_double, _p, _p, _p, _i32, _i64, _p,
+                                     _p, _p, _p, _p, _sz, _p]),
         "dg_sfc_workspace_size": (_sz, [_i64]),
         "dg_sfc_keys": (_i32, [_p, _i64, _i32, _p, _p, _sz, _p]),
         "dg_sfc_order": (_i32, [_p, _i64, _p, _p, _sz, _p]),

@@ -14,10 +14,12 @@
 #include <stdint.h>
 #include <string.h>
 
+#include <algorithm>
 #include <string>
 
 #include "../../include/dynamis_graph.h"
 #include "dg_common.hpp"
+#include "dg_lookback.hpp"
 #include "dg_scan.hpp"
 
 namespace dg {
@@ -319,10 +321,15 @@ __global__ void filter_clear_kernel(int* __restrict__ bad)
     if (threadIdx.x == 0) *bad = 0;
 }
 
-// n_kept = -1 when an edge named an atom outside [0, n)
+// n_kept = -1 when an edge named an atom outside [0, n); -2 when a look-back gave up
 __global__ void filter_bad_kernel(const int* __restrict__ bad, int64_t* __restrict__ n_kept)
 {
-    if (threadIdx.x == 0 && *bad) *n_kept = -1;
+    if (threadIdx.x == 0 && *bad) *n_kept = (*bad & 1) ? -1 : -2;
+}
+
+__global__ void zero_one_kernel(int64_t* __restrict__ p)
+{
+    if (threadIdx.x == 0) *p = 0;
 }
 
 // Two-pass compaction (count, then write in order): a workgroup of 256 threads takes
@@ -397,6 +404,135 @@ __global__ __launch_bounds__(256) void filter_write_kernel(const void* __restric
         odst[o] = d[k];
         for (int c = 0; c < 3; ++c) osh[3 * o + c] = sh[3 * (e0 + k) + c];
         ++o;
+    }
+}
+
+// ---- single-pass compaction (decoupled look-back, dg_lookback.hpp)
+// A workgroup takes a ticket t (its tile: edges [t kF1Tile, (t + 1) kF1Tile)), evaluates
+// the predicate on its kF1Per edges per thread (thread i holds edges i, i + kF1Threads, ...; all
+// their loads issued together), publishes its kept count, looks back for the kept count
+// of the tiles before it and writes its kept edges there, in order.  One read of the edge
+// list, one write of the kept edges.
+// 512 threads x 8 edges per tile: measured at C3 (115M edges) against 256 x 4 (2.51 ms),
+// 256 x 8 (2.24-2.40), 512 x 4 (2.32), 1024 x 4 (2.71), 1024 x 8 (2.18) and persistent
+// workgroups with a prefetched ticket (3.2 ms): 2.10 ms.
+constexpr int kF1Per = 8;
+constexpr int kF1Threads = 512;
+constexpr int kF1Tile = kF1Threads * kF1Per;
+constexpr int kF1Groups = kF1Per / 4;
+static_assert(kF1Per % 4 == 0, "kept flags are scanned four strides per uint64");
+
+__device__ __forceinline__ uint64_t lb_load(const uint64_t* p)
+{
+    return __hip_atomic_load(p, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+__device__ __forceinline__ void lb_store(uint64_t* p, uint64_t v)
+{
+    __hip_atomic_store(p, v, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT);
+}
+
+// Clears the ticket counter, the error flags and the status words of the tiles.
+__global__ void filter1_clear_kernel(uint64_t* __restrict__ status, int64_t ntiles,
+                                     unsigned* __restrict__ ticket, int* __restrict__ bad)
+{
+    const int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (i < ntiles) status[i] = 0;
+    if (i == 0) {
+        *ticket = 0u;
+        *bad = 0;
+    }
+}
+
+template <typename ST>
+__global__ __launch_bounds__(kF1Threads) void filter1_kernel(const void* __restrict__ pos, int f64,
+                                                             int64_t na, FilterCell C, double r2,
+                                                             const int64_t* __restrict__ src,
+                                                             const int64_t* __restrict__ dst,
+                                                             const ST* __restrict__ sh, int sdt,
+                                                             int64_t E, int64_t ntiles,
+                                                             uint64_t* __restrict__ status,
+                                                             unsigned* __restrict__ ticket,
+                                                             int* __restrict__ bad,
+                                                             int64_t* __restrict__ osrc,
+                                                             int64_t* __restrict__ odst,
+                                                             ST* __restrict__ osh,
+                                                             int64_t* __restrict__ n_kept)
+{
+    __shared__ unsigned s_t;
+    __shared__ uint64_t s_w[kF1Threads / 64];
+    __shared__ uint64_t s_win[lookback::kWindow];
+    __shared__ int64_t s_excl;
+    const int lane = threadIdx.x & 63;
+    if (threadIdx.x == 0) s_t = atomicAdd(ticket, 1u);
+    __syncthreads();
+    const int64_t t = s_t;
+    const int64_t e0 = t * kF1Tile + threadIdx.x;
+    // wave 0 walks back: every lane runs the same walk on the same window (one status word
+    // loaded per lane)
+    auto load = [&](int64_t i0, int m, uint64_t* w) {
+        __builtin_amdgcn_wave_barrier();  // every lane is done with the last window
+        w[lane] = lane < m ? lb_load(&status[i0 - lane]) : 0ull;
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+    };
+    int64_t s[kF1Per], d[kF1Per];
+    bool keep[kF1Per];
+#pragma unroll
+    for (int k = 0; k < kF1Per; ++k) {
+        const int64_t e = e0 + kF1Threads * k;
+        s[k] = e < E ? src[e] : 0;
+        d[k] = e < E ? dst[e] : 0;
+    }
+    // the first read of the predecessors' words, overlapping this tile's loads (no wait)
+    lookback::Walk W = lookback::walk_start(t);
+    if (threadIdx.x < 64) lookback::walk_step(W, s_win, load);
+    // kept flags of stride k packed as 16-bit fields, four strides per uint64: one scan per
+    // group of four yields, for every k, the kept edges of stride k before this thread (at
+    // most kF1Threads per field)
+    uint64_t packed[kF1Groups];
+#pragma unroll
+    for (int g = 0; g < kF1Groups; ++g) packed[g] = 0;
+#pragma unroll
+    for (int k = 0; k < kF1Per; ++k) {
+        const int64_t e = e0 + kF1Threads * k;
+        keep[k] = e < E && filter_keep(pos, f64, na, C, r2, s[k], d[k], sh, sdt, e, bad);
+        packed[k >> 2] |= (uint64_t)(keep[k] ? 1 : 0) << (16 * (k & 3));
+    }
+    uint64_t ex[kF1Groups], tot[kF1Groups];
+#pragma unroll
+    for (int g = 0; g < kF1Groups; ++g) ex[g] = block_excl_scan<uint64_t, kF1Threads>(packed[g], s_w, &tot[g]);
+    int64_t tile_total = 0;
+#pragma unroll
+    for (int k = 0; k < kF1Per; ++k) tile_total += (int64_t)((tot[k >> 2] >> (16 * (k & 3))) & 0xFFFFu);
+
+    if (threadIdx.x < 64) {  // wave 0: publish (AGGREGATE first if the walk is not done)
+        if (!W.done) {
+            if (lane == 0) lb_store(&status[t], lookback::word(lookback::kAggregate, tile_total));
+            auto wait = [] { __builtin_amdgcn_s_sleep(1); };
+            if (!lookback::walk_finish(W, s_win, load, wait, lookback::kMaxWaitSteps)) {
+                if (lane == 0) atomicOr(bad, 2);
+            }
+        }
+        if (lane == 0) {
+            lb_store(&status[t], lookback::word(lookback::kInclusive, W.sum + tile_total));
+            s_excl = W.sum;
+            if (t == ntiles - 1) *n_kept = W.sum + tile_total;
+        }
+    }
+    __syncthreads();
+    int64_t o = s_excl;
+#pragma unroll
+    for (int k = 0; k < kF1Per; ++k) {
+        const uint64_t fk = (ex[k >> 2] >> (16 * (k & 3))) & 0xFFFFu;
+        if (keep[k]) {
+            const int64_t q = o + (int64_t)fk;
+            const int64_t e = e0 + kF1Threads * k;
+            osrc[q] = s[k];
+            odst[q] = d[k];
+            for (int c = 0; c < 3; ++c) osh[3 * q + c] = sh[3 * e + c];
+        }
+        o += (int64_t)((tot[k >> 2] >> (16 * (k & 3))) & 0xFFFFu);
     }
 }
 
@@ -610,6 +746,58 @@ static Filter2Layout filter2_layout(int64_t E)
     L.o_bad = L.o_part + al(8 * (nb / kScanTile + 2));
     L.total = L.o_bad + al(8);
     return L;
+}
+
+// Workspace of the single-pass filter: ticket, error flags, one status word per tile.
+static size_t filter1_ws(int64_t E)
+{
+    const size_t nt = (size_t)((E + kF1Tile - 1) / kF1Tile);
+    return 256 + al(8 * (nt + 1));
+}
+
+size_t dg_filter_compact_workspace_size(int64_t E)
+{
+    if (E < 0) return 0;
+    return filter1_ws(E);
+}
+
+dg_status dg_filter_compact(const void* pos, int32_t pos_dtype, int64_t n_atoms, const double* cell,
+                            double radius, const int64_t* src, const int64_t* dst, const void* shift,
+                            int32_t shift_dtype, int64_t E, int64_t* out_src, int64_t* out_dst,
+                            void* out_shift, int64_t* n_kept, void* ws, size_t ws_bytes,
+                            hipStream_t s)
+{
+    dg_status st = filter_check(pos_dtype, shift_dtype, radius, E, n_atoms);
+    if (st != DG_OK) return st;
+    if (!n_kept) return fail(DG_ERR_INVALID, "n_kept is NULL");
+    if (ws_bytes < filter1_ws(E)) return fail(DG_ERR_WORKSPACE, "workspace too small");
+    const int64_t nt = (E + kF1Tile - 1) / kF1Tile;
+    char* w = (char*)ws;
+    unsigned* ticket = (unsigned*)w;
+    int* bad = (int*)(w + 64);
+    uint64_t* status = (uint64_t*)(w + 256);
+    if (nt > 0x7fffffffLL) return fail(DG_ERR_INVALID, "too many edges");
+    hipLaunchKernelGGL(filter1_clear_kernel, dim3(nt > 0 ? nblk(nt) : 1), dim3(256), 0, s, status, nt,
+                       ticket, bad);
+    if (nt == 0) {
+        hipLaunchKernelGGL(zero_one_kernel, dim3(1), dim3(64), 0, s, n_kept);
+        return launch_ok("dg_filter_compact");
+    }
+    const int f64 = (int)(pos_dtype == DG_F64);
+    const FilterCell C = filter_cell(cell);
+    const double r2 = radius * radius;
+#define DG_F1(T)                                                                                       \
+    hipLaunchKernelGGL(filter1_kernel<T>, dim3((unsigned)nt), dim3(kF1Threads), 0, s, pos, f64, n_atoms, \
+                       C, r2,                                                                          \
+                       src, dst, (const T*)shift, (int)shift_dtype, E, nt, status, ticket, bad, out_src,  \
+                       out_dst, (T*)out_shift, n_kept)
+    if (shift_dtype == DG_F32) DG_F1(float);
+    else if (shift_dtype == DG_F64) DG_F1(double);
+    else if (shift_dtype == DG_I32) DG_F1(int32_t);
+    else DG_F1(int64_t);
+#undef DG_F1
+    hipLaunchKernelGGL(filter_bad_kernel, dim3(1), dim3(64), 0, s, (const int*)bad, n_kept);
+    return launch_ok("dg_filter_compact");
 }
 
 size_t dg_filter2_workspace_size(int64_t E)

@@ -237,27 +237,29 @@ def filter_edges_to_radius(edges, cell_shifts, pos, cell, radius):
         sdt = L.DG_I64
     c = cell.detach().to(device="cpu", dtype=pos.dtype).to(torch.float64).contiguous()
     cbuf = (L.ctypes.c_double * 9)(*c.reshape(-1).tolist())
-    wsb = lib.dg_filter2_workspace_size(E)
     pdt = L.DG_F64 if pos.dtype == torch.float64 else L.DG_F32
     base = edges.data_ptr()
-    args = (L.ptr(pos), pdt, pos.size(0), cbuf, float(radius), L.ctypes.c_void_p(base),
-            L.ctypes.c_void_p(base + 8 * E), L.ptr(sh), sdt, E)
     with torch.cuda.device(dev):
         s = L.stream_of(dev)
+        wsb = lib.dg_filter_compact_workspace_size(E)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         nk = torch.empty(1, dtype=torch.int64, device=dev)
-        # pass 1: kept count per block of edges and their offsets; pass 2 (after the
-        # exact-size allocation): the kept edges, in order, straight into the outputs
-        L.check(lib.dg_filter_count(*args, L.ptr(nk), L.ptr(ws), wsb, s), "filter_edges_to_radius")
+        # One pass: the kept edges land in order in the first k rows of E-row outputs.  The
+        # sources go straight to row 0 of the result, the targets to a scratch row, moved
+        # behind them once k is known, so edge_index is [2, k] contiguous.
+        buf = torch.empty(2 * E, dtype=torch.int64, device=dev)
+        dst_tmp = torch.empty(E, dtype=torch.int64, device=dev)
+        out_s = torch.empty((E, 3), dtype=sh.dtype, device=dev)
+        L.check(lib.dg_filter_compact(L.ptr(pos), pdt, pos.size(0), cbuf, float(radius),
+                                      L.ctypes.c_void_p(base), L.ctypes.c_void_p(base + 8 * E), L.ptr(sh),
+                                      sdt, E, L.ptr(buf), L.ptr(dst_tmp), L.ptr(out_s), L.ptr(nk),
+                                      L.ptr(ws), wsb, s), "filter_edges_to_radius")
         k = int(nk.item())
-        _check(k >= 0, f"filter_edges_to_radius: edges hold atom indices outside [0, {pos.size(0)})")
-        out_e = torch.empty((2, k), dtype=torch.int64, device=dev)
-        out_s = torch.empty((k, 3), dtype=sh.dtype, device=dev)
-        if k > 0:
-            ob = out_e.data_ptr()
-            L.check(lib.dg_filter_write(*args, L.ptr(ws), wsb, L.ctypes.c_void_p(ob),
-                                        L.ctypes.c_void_p(ob + 8 * k), L.ptr(out_s), s),
-                    "filter_edges_to_radius")
+        _check(k != -1, f"filter_edges_to_radius: edges hold atom indices outside [0, {pos.size(0)})")
+        _check(k >= 0, "filter_edges_to_radius: internal error (a block's wait for its predecessors gave up)")
+        buf[k:2 * k].copy_(dst_tmp[:k])
+        out_e = buf[:2 * k].view(2, k)
+        out_s = out_s[:k]
         if out_s.dtype != cell_shifts.dtype:
             out_s = out_s.to(cell_shifts.dtype)
         return out_e, out_s

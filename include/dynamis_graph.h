@@ -171,6 +171,22 @@ dg_status dg_filter_write(const void* pos, int32_t pos_dtype, int64_t n_atoms, c
                           const void* workspace, size_t workspace_bytes, int64_t* out_src,
                           int64_t* out_dst, void* out_shift, hipStream_t stream);
 
+/* The same filter in one pass over the edge list (a decoupled look-back gives each block
+ * of 4096 edges the kept count before it): kept edges go, in order, to the first n_kept
+ * rows of outputs of capacity n_edges.  Replaces the same reference function; the form
+ * the Python filter_edges_to_radius uses.
+ *   out_src/out_dst int64 [n_edges], out_shift [n_edges,3] of shift_dtype (capacity)
+ *   n_kept  out int64 (device, one value): -1 if an edge names an atom outside
+ *           [0, n_atoms), -2 if a block's wait for its predecessors gave up (a bounded wait;
+ *           not expected), else the number of kept edges
+ *   workspace of dg_filter_compact_workspace_size(n_edges) bytes */
+size_t dg_filter_compact_workspace_size(int64_t n_edges);
+dg_status dg_filter_compact(const void* pos, int32_t pos_dtype, int64_t n_atoms, const double* cell,
+                            double radius, const int64_t* edge_src, const int64_t* edge_dst,
+                            const void* cell_shift, int32_t shift_dtype, int64_t n_edges,
+                            int64_t* out_src, int64_t* out_dst, void* out_shift, int64_t* n_kept,
+                            void* workspace, size_t workspace_bytes, hipStream_t stream);
+
 /* SFC keys exactly as partition/sfc_kernels.cu:19-109 (curve 0 = Morton 21-bit,
  * 1 = "Hilbert" order 7), normalised by the global min / range of pos
  * (sfc_kernels.cu:196-198, range 0 -> 1).  pos fp32 [n,3]; keys int64 [n];
