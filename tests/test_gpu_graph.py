@@ -217,10 +217,28 @@ def test_wrapped_and_far_positions(cuda):
 
 
 def test_all_pairs_fallback(cuda):
-    # r >> cell: the search region would exceed the LDS table -> all-pairs kernel
+    # r >> cell: at r = 10 in a 3 A cell the stencil is 9^3 copies of one bin (the largest
+    # region the tiled path takes); at r = 13 it would exceed that -> all-pairs kernel
     pos, cell = _rand(7, 3.0, 9)
+    check_parity(pos, cell, (1, 1, 1), 13.0, cuda, name="all-pairs r=13")
     check_parity(pos, cell, (1, 1, 1), 10.0, cuda, name="all-pairs")
     check_parity(pos, cell, (1, 0, 1), 10.0, cuda, name="all-pairs partial")
+
+
+def test_all_pairs_fallback_many_atoms(cuda):
+    """The all-pairs kernel (a stencil of more than 768 bins: r > 4 cell widths) on tens of
+    atoms with tens of thousands of periodic-image neighbours each, orthorhombic and
+    triclinic, full and partial PBC; and the many-chunk sweep just below that limit (r = 10
+    in a 6 A cell: one bin, a 5x5x5 stencil of its periodic copies)."""
+    pos, cell = _rand(60, 3.0, 31)
+    _, _, cnt, _ = check_parity(pos, cell, (1, 1, 1), 13.0, cuda, name="all-pairs 60")
+    assert int(cnt.min()) > 15000
+    tri = np.array([[3.0, 0.0, 0.0], [0.8, 2.8, 0.0], [-0.5, 0.4, 3.1]])
+    pos, _ = _rand(40, 1.0, 32, dtype=np.float64, cell=tri)
+    check_parity(pos, tri, (1, 0, 1), 13.0, cuda, name="all-pairs triclinic partial pbc")
+    pos, cell = _rand(300, 6.0, 33)
+    _, _, cnt, _ = check_parity(pos, cell, (1, 1, 1), 10.0, cuda, name="one bin, 125 copies")
+    assert int(cnt.min()) > 3000
 
 
 def test_dense_multichunk_and_oversized_targets(cuda):
