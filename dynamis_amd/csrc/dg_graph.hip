@@ -270,8 +270,10 @@ __device__ __forceinline__ void sort_chunk(int64_t n, int64_t* lo, int64_t* hi)
 
 __global__ __launch_bounds__(1024) void tile_hist_kernel(int64_t n, int tb, int64_t ntiles,
                                                          const uint32_t* __restrict__ key,
-                                                         int* __restrict__ tcnt, int* __restrict__ wgb)
+                                                         int* __restrict__ tcnt, int* __restrict__ wgb,
+                                                         const int64_t* __restrict__ run_if)
 {
+    if (run_if && *run_if == 0) return;  // (explicit targets that need no sort)
     extern __shared__ int h[];
     for (int64_t r = threadIdx.x; r < ntiles; r += blockDim.x) h[r] = 0;
     __syncthreads();
@@ -304,8 +306,10 @@ __global__ __launch_bounds__(1024) void tile_scatter_kernel(int64_t n, int tb, i
                                                             const int* __restrict__ tcnt,
                                                             int* __restrict__ tstart,
                                                             const int* __restrict__ wgb,
-                                                            BT* __restrict__ bucket)
+                                                            BT* __restrict__ bucket,
+                                                            const int64_t* __restrict__ run_if)
 {
+    if (run_if && *run_if == 0) return;  // (explicit targets that need no sort)
     extern __shared__ int h[];  // this chunk's next place in every tile's bucket
     __shared__ int s_w[1024 / 64];
     {
@@ -374,6 +378,7 @@ struct TileSortOut {
     int64_t natoms;
     int* tslot;
     int* tsidx;
+    const int64_t* run_if;  // targets: skipped when *run_if == 0 (they need no sort)
 };
 
 // One workgroup per tile: orders its bucket by (bin, id), writes the tile's bin starts and
@@ -385,6 +390,7 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
                                                         const BT* __restrict__ bucket,
                                                         int* __restrict__ bstart, TileSortOut o)
 {
+    if (o.run_if && *o.run_if == 0) return;
     __shared__ TileSortLds S;
     typedef typename std::conditional<TGT, int, float4>::type Pay;
     auto gather = [&](int i) -> Pay {
@@ -478,6 +484,7 @@ __global__ void target_keys_kernel(int64_t nt, int64_t n, const int64_t* __restr
                                    const uint32_t* __restrict__ key, uint32_t* __restrict__ tkey,
                                    int* __restrict__ tcnt, int64_t ntiles, int64_t* __restrict__ totals)
 {
+    if (totals[2] == 0) return;  // the targets are 0 .. nt - 1: no sort (target_prefix_kernel)
     const int64_t stride = (int64_t)gridDim.x * blockDim.x;
     const int64_t i0 = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     for (int64_t r = i0; r < ntiles; r += stride) tcnt[r] = 0;
@@ -489,6 +496,20 @@ __global__ void target_keys_kernel(int64_t nt, int64_t n, const int64_t* __restr
         }
         tkey[t] = key[a];
     }
+}
+
+// Raises totals[2] unless the explicit targets are exactly 0, 1, ..., nt - 1 with nt <= n
+// (then the count takes the atoms of each tile with ids < nt as its targets, in cell-list
+// order, with no target sort).  totals[2] was cleared by tile_rank_kernel.
+__global__ void target_prefix_kernel(int64_t nt, int64_t n, const int64_t* __restrict__ tgt,
+                                     int64_t* __restrict__ totals)
+{
+    const int64_t stride = (int64_t)gridDim.x * blockDim.x;
+    bool other = nt > n;
+    for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nt && !other; t += stride)
+        other = tgt[t] != t;
+    if (__builtin_amdgcn_ballot_w64(other) != 0ull && (threadIdx.x & 63) == 0)
+        atomicOr((unsigned long long*)&totals[2], 1ull);
 }
 
 __global__ void bin_targets_kernel(int64_t nt, int64_t n, const int64_t* __restrict__ tgt,
@@ -561,6 +582,12 @@ struct SearchArgs {
     int f64;
     // explicit targets (subset != 0)
     int subset;
+    // Explicit targets that are exactly 0, 1, ..., ntarg - 1 (checked on the device: the
+    // local atoms of a partition, DistGraphBuilder's mode B) need no target sort: every atom
+    // of a tile is a lane, and atoms with ids >= ntarg (the ghosts) stay idle.  pmis is the
+    // device word that is nonzero when the list is not that prefix (null: never masked).
+    const int64_t* pmis;
+    int64_t ntarg;
     const int* tbstart;
     const int* tsidx;
     const int* tslot;  // caller position of each sorted target
@@ -586,6 +613,17 @@ struct SearchArgs {
     int K;
     int64_t nslot;  // targets (group row length)
 };
+
+// Whether this build's targets are the atoms of the tile with ids < ntarg (see SearchArgs).
+__device__ __forceinline__ bool masked_targets(const SearchArgs& a)
+{
+    return a.subset && a.pmis != nullptr && *a.pmis == 0;
+}
+// Whether targets come from the explicit (sorted) target list.
+__device__ __forceinline__ bool listed_targets(const SearchArgs& a)
+{
+    return a.subset && !masked_targets(a);
+}
 
 // Output order -> tile rank: consecutive workgroups go round-robin to the 8 XCDs, so
 // give each XCD one contiguous range of the Morton order (its own compact region of space, so the halo bins a tile
@@ -852,7 +890,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
         int btot;
         const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
         if (active) {
-            const int sidx = a.subset ? a.tsidx[j] : j;
+            const int sidx = listed_targets(a) ? a.tsidx[j] : j;
             B.off[threadIdx.x] = ex;
             B.tid[threadIdx.x] = a.sid[sidx];
             B.tf[threadIdx.x] = a.sflr[sidx];
@@ -1086,7 +1124,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
     const int ty = (lin / a.ntl[0]) % a.ntl[1];
     const int tz = lin / (a.ntl[0] * a.ntl[1]);
     const int g0[3] = {tx * a.T[0], ty * a.T[1], tz * a.T[2]};
-    const int* tstart = a.subset ? a.tbstart : a.bstart;
+    const bool listed = listed_targets(a), masked = a.subset && !listed;
+    const int* tstart = listed ? a.tbstart : a.bstart;
     const int64_t kb = rank * a.tb;
     const int tbeg = tstart[kb], tend = tstart[kb + a.tb];
     const int ntg = tend - tbeg;
@@ -1101,6 +1140,18 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         return out;
     }
     if (WRITE && (a.tfix[ord] & (kFixOver | kFixChunked)) == 0) return out;  // written by an expansion
+    if (!WRITE && masked) {
+        // a tile of ghosts only (atoms with ids >= ntarg) has no targets: nothing to count
+        bool mine = false;
+        for (int k = threadIdx.x; k < ntg; k += kBlock) mine = mine || a.sid[tbeg + k] < a.ntarg;
+        if (!block_any<kBlock>(mine, sh.w32)) {
+            if (threadIdx.x == 0) {
+                a.ttot[ord] = 0;
+                a.tfix[ord] = 0;
+            }
+            return out;
+        }
+    }
     for (int k = threadIdx.x; k <= a.tb; k += kBlock) sh.tbs[k] = tstart[kb + k];
 
     int64_t ebase = 0;
@@ -1193,7 +1244,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         const int nbatch = min(kBlock, ntg - k0);
         const int kk = k0 + threadIdx.x;
         const int j = tbeg + kk;
-        const bool active = threadIdx.x < nbatch;
+        const bool in_batch = threadIdx.x < nbatch;
+        bool active = in_batch;
 
         // ---- per-lane target state
         int lx = 0, ly = 0, lz = 0, my_id = 0, caller = 0, v_self = -1;
@@ -1208,18 +1260,19 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             lx = lo % a.T[0];
             ly = (lo / a.T[0]) % a.T[1];
             lz = lo / (a.T[0] * a.T[1]);
-            const int sidx = a.subset ? a.tsidx[j] : j;
+            const int sidx = listed ? a.tsidx[j] : j;
             const float4 e = a.spos[sidx];
             my_f = a.sflr[sidx];
             my_id = __float_as_int(e.w);
-            caller = a.subset ? a.tslot[j] : my_id;
+            caller = listed ? a.tslot[j] : my_id;
+            active = !masked || my_id < a.ntarg;  // (masked: a ghost atom's lane idles)
             ux = e.x; uy = e.y; uz = e.z;  // position inside its own bin
             float o[3];
             region_offset(a, lx + a.P[0], ly + a.P[1], lz + a.P[2], o);
             t0 = e.x + o[0]; t1 = e.y + o[1]; t2 = e.z + o[2];
             // the target's own region entry (same atom, zero shift) is never an edge
             const int rb_self = ((lz + a.P[2]) * R1 + (ly + a.P[1])) * R0 + (lx + a.P[0]);
-            const int bin_start = a.subset ? a.bstart[kb + lo] : sh.tbs[lo];
+            const int bin_start = listed ? a.bstart[kb + lo] : sh.tbs[lo];
             v_self = sh.rp[rb_self] + (sidx - bin_start);
         }
         const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
@@ -1417,6 +1470,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 if (a.counts_user) a.counts_user[caller] = found;
                 tile_found += found;
                 over_any = over_any || found > a.K;
+            } else if (in_batch) {
+                a.cnt[j] = 0;  // (masked: a ghost, no edges)
             }
             __syncthreads();
             continue;
@@ -1490,11 +1545,11 @@ __device__ __forceinline__ void expand_one(const SearchArgs& a, typename ExpandL
                                            int64_t ord)
 {
     const int64_t rank = xcd_tile_rank(ord, a.ntiles);
-    const int* tstart = a.subset ? a.tbstart : a.bstart;
+    const int* tstart = listed_targets(a) ? a.tbstart : a.bstart;
     const int64_t kb = rank * a.tb;
     const int tbeg = tstart[kb], tend = tstart[kb + a.tb];
     const int ntg = tend - tbeg;
-    if (ntg == 0) return;
+    if (ntg == 0 || a.ttot[ord] == 0) return;  // (no edges: nothing to expand)
     const int64_t ebase = a.tbase[ord];
     if (ebase + a.ttot[ord] > a.capacity) {
         if (threadIdx.x == 0)
@@ -1819,9 +1874,16 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.tbase = at<int64_t>(ws, p.o_tbase);
     a.totals = at<int64_t>(ws, p.o_tot);
     // slots are addressed with 32-bit byte offsets; larger problems sweep twice instead
-    a.slot = 2.0 * p.K * (double)p.nt < 4294967296.0 ? at<uint16_t>(ws, p.o_slot) : nullptr;
+    // slot rows: one per target, or per atom when the targets are the atoms with ids < nt
+    // (every atom of a tile is then a lane)
+    const int64_t nrow = p.nrow;
+    a.slot = 2.0 * p.K * (double)nrow < 4294967296.0 ? at<uint16_t>(ws, p.o_slot) : nullptr;
     a.K = p.K;
-    a.nslot = p.nt;
+    a.nslot = nrow;
+    a.ntarg = p.nt;
+    // the prefix test runs with the tile-level sort only (the per-bin fallback sorts the
+    // explicit targets as listed)
+    a.pmis = p.subset && p.ntiles <= kSortTilesMax ? at<int64_t>(ws, p.o_tot) + 2 : nullptr;
     return a;
 }
 
@@ -1885,16 +1947,17 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         // 32-bit bucket entries when every id (atom, and target position) fits 24 bits
         const bool narrow = p.n < (1 << 24) && (!p.subset || p.nt < (1 << 24));
         allow_dyn_lds(narrow ? (const void*)tile_scatter_kernel<uint32_t> : (const void*)tile_scatter_kernel<uint64_t>, hl);
+        const int64_t* always = nullptr;
         hipLaunchKernelGGL(tile_hist_kernel, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
-                           (const uint32_t*)at<uint32_t>(ws, p.o_key), tcnt, wgb);
+                           (const uint32_t*)at<uint32_t>(ws, p.o_key), tcnt, wgb, always);
         if (narrow)
             hipLaunchKernelGGL(tile_scatter_kernel<uint32_t>, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
                                (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)tcnt, tstart,
-                               (const int*)wgb, at<uint32_t>(ws, p.o_arr));
+                               (const int*)wgb, at<uint32_t>(ws, p.o_arr), always);
         else
             hipLaunchKernelGGL(tile_scatter_kernel<uint64_t>, dim3(nch), dim3(1024), hl, s, p.n, p.tb, p.ntiles,
                                (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)tcnt, tstart,
-                               (const int*)wgb, at<uint64_t>(ws, p.o_arr));
+                               (const int*)wgb, at<uint64_t>(ws, p.o_arr), always);
         TileSortOut o;
         memset(&o, 0, sizeof o);
         o.rec = at<float4>(ws, p.o_rec);
@@ -1910,22 +1973,27 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
                                p.tb, p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_arr), bstart, o);
         if (p.subset) {
             // the explicit targets through the same tile-level sort: keyed by their atom's
-            // bin, ordered by caller position inside a bin
+            // bin, ordered by caller position inside a bin -- unless they are exactly
+            // 0 .. nt - 1 (target_prefix_kernel leaves totals[2] at 0): then the kernels below
+            // exit at once and the count takes the atoms of each tile with ids < nt
+            hipLaunchKernelGGL(target_prefix_kernel, dim3((unsigned)std::min<int64_t>(nblocks(p.nt), 2048)), dim3(256),
+                               0, s, p.nt, p.n, target_idx, totals);
+            const int64_t* listed = totals + 2;
             uint32_t* tkey = at<uint32_t>(ws, p.o_tkey);
             hipLaunchKernelGGL(target_keys_kernel, dim3((unsigned)std::min<int64_t>(nblocks(std::max(p.nt, p.ntiles)), 4096)),
                                dim3(256), 0, s, p.nt, p.n, target_idx, (const uint32_t*)at<uint32_t>(ws, p.o_key),
                                tkey, tcnt, p.ntiles, totals);
             const unsigned tch = (unsigned)std::max<int64_t>(1, std::min<int64_t>(kSortChunks, (p.nt + 4095) / 4096));
             hipLaunchKernelGGL(tile_hist_kernel, dim3(tch), dim3(1024), hl, s, p.nt, p.tb, p.ntiles,
-                               (const uint32_t*)tkey, tcnt, wgb);
+                               (const uint32_t*)tkey, tcnt, wgb, listed);
             if (narrow)
                 hipLaunchKernelGGL(tile_scatter_kernel<uint32_t>, dim3(tch), dim3(1024), hl, s, p.nt, p.tb, p.ntiles,
                                    (const uint32_t*)tkey, (const int*)tcnt, tstart, (const int*)wgb,
-                                   at<uint32_t>(ws, p.o_tarr));
+                                   at<uint32_t>(ws, p.o_tarr), listed);
             else
                 hipLaunchKernelGGL(tile_scatter_kernel<uint64_t>, dim3(tch), dim3(1024), hl, s, p.nt, p.tb, p.ntiles,
                                    (const uint32_t*)tkey, (const int*)tcnt, tstart, (const int*)wgb,
-                                   at<uint64_t>(ws, p.o_tarr));
+                                   at<uint64_t>(ws, p.o_tarr), listed);
             TileSortOut ot;
             memset(&ot, 0, sizeof ot);
             ot.inv = at<int>(ws, p.o_inv);
@@ -1933,6 +2001,7 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
             ot.natoms = p.n;
             ot.tslot = at<int>(ws, p.o_tslot);
             ot.tsidx = at<int>(ws, p.o_tsidx);
+            ot.run_if = listed;
             if (narrow)
                 hipLaunchKernelGGL((tile_sort_kernel<true, uint32_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s,
                                    p.nt, p.tb, p.ntiles, (const int*)tstart,

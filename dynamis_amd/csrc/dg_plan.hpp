@@ -55,6 +55,7 @@ struct Plan {
     size_t o_tkey, o_trank, o_tbcnt, o_tbstart, o_tslot, o_tsidx, o_tcaller;
     size_t o_cnt, o_ttot, o_tfix, o_tbase, o_part, o_tot, o_slot;
     int K = 0;              // neighbour slot entries per target
+    int64_t nrow = 0;       // slot rows (group-major row length)
     size_t ws_bytes = 0;
 };
 
@@ -269,8 +270,14 @@ inline void plan_layout(Plan& p)
     p.o_tarr = take(p.subset ? 8 * nt : 0);
     p.o_tsidx = take(p.subset ? 4 * nt : 0);
     p.o_tcaller = take(p.subset ? 4 * nt : 0);
-    p.o_cnt = take(4 * nt);
-    p.o_slot = take(2 * (size_t)p.K * nt);
+    // per-target counts and slots: one row per target, or per atom when explicit targets
+    // turn out to be the atoms 0 .. nt - 1 (the count then runs over every atom of a tile)
+    // (rows padded to 256 targets: the group rows of a row length of 2 mod 4 targets, e.g.
+    // C5's 4,436,018 atoms, made the expansion 5 % slower, 3.02 against 2.87 ms)
+    const size_t nrow = (std::max(n, nt) + 255) / 256 * 256;
+    p.nrow = (int64_t)nrow;
+    p.o_cnt = take(4 * nrow);
+    p.o_slot = take(2 * (size_t)p.K * nrow);
     p.o_ttot = take(4 * std::max(ntl, nt));
     p.o_tfix = take(4 * ntl);
     p.o_tbase = take(8 * (std::max(ntl, nt) + 1));

@@ -256,6 +256,45 @@ def test_explicit_targets_with_duplicates(cuda):
     check_parity(box.pos, box.cell, box.pbc, box.radius, cuda, targets=tg, name="targets")
 
 
+def test_prefix_targets(cuda):
+    """Explicit targets 0 .. nt - 1 (the local atoms of a partition) take the count over
+    every atom of a tile with the ghosts' lanes idle, instead of a target sort.  With
+    nt = n the result is byte-identical to the build without targets; with nt < n it
+    equals the same target set given in another order (the sorted path), edge set and
+    per-target counts."""
+    _announce("prefix targets")
+    box = configs.uniform(30000, seed=26, dtype=np.float32)
+    p = torch.from_numpy(box.pos).to(cuda)
+    c = torch.from_numpy(box.cell)
+    b = torch.tensor([True] * 3)
+    n = len(box.pos)
+    full = impl.radius_graph_pbc_ex(p, c, b, box.radius, 0, False)
+    pref = impl.radius_graph_pbc_ex(p, c, b, box.radius, 0, False, torch.arange(n, device=cuda))
+    for x, y in zip(full, pref):
+        assert torch.equal(x, y)
+    box = configs.c5(n_owned=30_000, side=66.9)
+    p = torch.from_numpy(box.pos).to(cuda)
+    c = torch.from_numpy(np.asarray(box.cell, np.float64))
+    b = torch.tensor(list(box.pbc))
+    nt = len(box.targets)
+    t1 = torch.arange(nt, device=cuda)
+    t2 = t1.clone()
+    t2[[0, nt - 1]] = t2[[nt - 1, 0]]  # not the prefix: the sorted-target path
+    e1, s1, _, c1 = impl.radius_graph_pbc_ex(p, c, b, box.radius, 0, False, t1)
+    e2, s2, _, c2 = impl.radius_graph_pbc_ex(p, c, b, box.radius, 0, False, t2)
+    c2 = c2.clone()
+    c2[[0, nt - 1]] = c2[[nt - 1, 0]]
+    assert torch.equal(c1, c2)
+    g1 = oracle.canonical_sort(e1[0].cpu().numpy(), e1[1].cpu().numpy(), s1.cpu().numpy().astype(np.int64))
+    g2 = oracle.canonical_sort(e2[0].cpu().numpy(), e2[1].cpu().numpy(), s2.cpu().numpy().astype(np.int64))
+    for x, y in zip(g1, g2):
+        assert np.array_equal(x, y)
+    # and nt = 0 .. a few: tiny prefixes
+    for k in (1, 7):
+        _, _, _, ck = impl.radius_graph_pbc_ex(p, c, b, box.radius, 0, False, torch.arange(k, device=cuda))
+        assert torch.equal(ck, c1[:k])
+
+
 def test_counts_only_matches(cuda):
     box = configs.uniform(20000, seed=3, dtype=np.float32)
     p = torch.from_numpy(box.pos).to(cuda)
