@@ -2216,12 +2216,21 @@ static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxDevices];
 
 // The scratch address on the current device, looked up once per device.
-static dg_status scratch_on_current_device(void** out)
+// The stream must belong to the current device: the address is that device's copy.
+static dg_status scratch_on_current_device(hipStream_t s, void** out)
 {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
     if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
     if (dev < 0 || dev >= kMaxDevices) return fail(DG_ERR_INVALID, "device ordinal out of range");
+    if (s != nullptr) {
+        hipDevice_t sdev = -1;
+        e = hipStreamGetDevice(s, &sdev);
+        if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipStreamGetDevice: ") + hipGetErrorString(e));
+        if (sdev != dev)
+            return fail(DG_ERR_INVALID, "dg_graph_build_noalloc: the stream belongs to device " +
+                                            std::to_string(sdev) + ", the current device is " + std::to_string(dev));
+    }
     std::lock_guard<std::mutex> lock(g_scratch_mu);
     if (!g_scratch_ptr[dev]) {
         void* ptr = nullptr;
@@ -2258,7 +2267,7 @@ extern "C" dg_status dg_graph_build_noalloc(const dg_graph_desc* desc, const voi
                                           "scratch holds " + std::to_string(kScratchBytes) +
                                           " (use dg_graph_build with a caller workspace)");
     void* ws = nullptr;
-    st = scratch_on_current_device(&ws);
+    st = scratch_on_current_device(s, &ws);
     if (st != DG_OK) return st;
     st = dg_graph_build(desc, pos, target_idx, ws, kScratchBytes, capacity, counts_out, edge_src,
                         edge_dst, cell_shift, edge_vec, edge_dist, vec_dtype, s);

@@ -127,7 +127,8 @@ dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64
  * which the caller reads when it needs them (an edge count above `capacity`, or
  * DG_FLAG_CAPACITY, means the tiles that did not fit were skipped).  Every call on one
  * GPU shares that GPU's array: calls that overlap on one GPU (two streams, two host
- * threads) race and must be serialised by the caller. */
+ * threads) race and must be serialised by the caller.  The stream must belong to the
+ * current device (DG_ERR_INVALID otherwise). */
 dg_status dg_graph_build_noalloc(const dg_graph_desc* desc, const void* pos,
                                  const int64_t* target_idx, int64_t capacity, int32_t* counts_out,
                                  int64_t* edge_src, int64_t* edge_dst, float* cell_shift,
