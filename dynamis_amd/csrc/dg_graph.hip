@@ -38,6 +38,7 @@
 #include "dg_common.hpp"
 #include "dg_plan.hpp"
 #include "dg_scan.hpp"
+#include "dg_segsort.hpp"
 
 // The count kernel (search_kernel<0>) is compiled in a translation unit of its own,
 // dg_count.hip, which includes this file with DG_COUNT_TU defined: there, only the
@@ -225,11 +226,35 @@ __device__ __forceinline__ void small_sort(int* a, int lo, int hi)
     }
 }
 
+// Sorts every segment [start[b], start[b + 1]) of v longer than kBinSortMax (by value,
+// ascending; ids < 2^31) in place, tmp its scratch: the bins that order_atoms_kernel and
+// finish_targets_kernel leave as they are.  Workgroup g scans its own range of segments,
+// 256 at a time, and sorts the long ones of each batch in turn.
+__global__ __launch_bounds__(kSegSortThreads) void sort_big_bins_kernel(int64_t nseg, const int* __restrict__ start,
+                                                                        uint32_t* __restrict__ v,
+                                                                        uint32_t* __restrict__ tmp)
+{
+    __shared__ SegSortLds L;
+    __shared__ int big[kSegSortThreads];
+    const int64_t per = (nseg + gridDim.x - 1) / gridDim.x;
+    const int64_t b0 = (int64_t)blockIdx.x * per, b1 = min(nseg, b0 + per);
+    for (int64_t c = b0; c < b1; c += kSegSortThreads) {
+        const int64_t b = c + threadIdx.x;
+        big[threadIdx.x] = b < b1 && start[b + 1] - start[b] > kBinSortMax;
+        __syncthreads();
+        for (int k = 0; k < kSegSortThreads; ++k) {
+            if (!big[k]) continue;  // (the same for every thread)
+            const int lo = start[c + k], hi = start[c + k + 1];
+            segment_sort<uint32_t>(v + lo, tmp + lo, hi - lo, 32, L);
+        }
+        __syncthreads();
+    }
+}
+
 // One thread per cell-list entry j (in arrival order inside its bin, from scatter_atoms):
 // the entry's place in its bin ordered by atom id (the number of smaller ids in the bin),
-// then the SoA cell list.  Bins with more than kBinSortMax atoms keep the atomic arrival
-// order (edge set and counts are unaffected; only the order of edges within a target can
-// then vary).
+// then the SoA cell list.  Bins of more than kBinSortMax atoms were put in id order by
+// sort_big_bins_kernel already: there the place is j.
 __global__ void order_atoms_kernel(int64_t n, const uint32_t* __restrict__ key,
                                    const int* __restrict__ bstart, const int* __restrict__ arr,
                                    const float4* __restrict__ rec, float4* __restrict__ spos,
@@ -356,9 +381,14 @@ __global__ __launch_bounds__(1024) void tile_scatter_kernel(int64_t n, int tb, i
 constexpr int kTileSortCap = 2048;  // bucket entries ordered in LDS (larger: arrival order in bins)
 constexpr int kTileSortPer = kTileSortCap / 256;
 struct TileSortLds {
-    int id[kTileSortCap];
-    int lb[kTileSortCap];
-    int by[kTileSortCap];  // ids grouped by bin
+    union {
+        struct {
+            int id[kTileSortCap];
+            int lb[kTileSortCap];
+            int by[kTileSortCap];  // ids grouped by bin
+        };
+        SegSortLds seg;  // a larger bucket: sorted in global memory
+    };
     int cnt[kTileMax * kTileMax * kTileMax];
     int st[kTileMax * kTileMax * kTileMax + 1];
     int w32[4];
@@ -379,6 +409,7 @@ struct TileSortOut {
     int* tslot;
     int* tsidx;
     const int64_t* run_if;  // targets: skipped when *run_if == 0 (they need no sort)
+    void* stmp;             // scratch for a bucket of more than kTileSortCap entries (one per entry)
 };
 
 // One workgroup per tile: orders its bucket by (bin, id), writes the tile's bin starts and
@@ -387,7 +418,7 @@ struct TileSortOut {
 template <bool TGT, typename BT>
 __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64_t ntiles,
                                                         const int* __restrict__ tstart,
-                                                        const BT* __restrict__ bucket,
+                                                        BT* __restrict__ bucket,
                                                         int* __restrict__ bstart, TileSortOut o)
 {
     if (o.run_if && *o.run_if == 0) return;
@@ -454,11 +485,12 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
         }
     };
     if (!fits) {
-        // a very dense tile: bins in arrival order, payloads gathered here
+        // a very dense tile: the bucket sorted by (bin, id) in global memory (an entry's
+        // bin sits above its id), then each entry goes to its place
+        segment_sort<BT>(bucket + base, (BT*)o.stmp + base, m, sizeof(BT) == 4 ? 32 : 40, S.seg);
         for (int e = threadIdx.x; e < m; e += 256) {
-            const BT w = bucket[base + e];
-            const int i = bk_id(w);
-            emit(base + atomicAdd(&S.cnt[bk_bin(w)], 1), i, gather(i));
+            const int i = bk_id(bucket[base + e]);
+            emit(base + e, i, gather(i));
         }
         return;
     }
@@ -1925,6 +1957,12 @@ static void allow_dyn_lds(const void* fn, size_t bytes)
         done.emplace_back(fn, bytes);
 }
 
+// Workgroups of sort_big_bins_kernel: about 1024 bins each, at most 2048.
+static unsigned big_bins_grid(int64_t nbins)
+{
+    return (unsigned)std::max<int64_t>(1, std::min<int64_t>(2048, (nbins + 1023) / 1024));
+}
+
 // Steps 1-5 of a build: Morton tile ranks, counting sort of the atoms (and of the
 // explicit targets) into the SFC-ordered cell list.
 void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void* ws,
@@ -1970,12 +2008,13 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         o.sflr = at<uint32_t>(ws, p.o_sflr);
         o.sid = at<int>(ws, p.o_sid);
         o.inv = p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr;
+        o.stmp = at<void>(ws, p.o_stmp);
         if (narrow)
             hipLaunchKernelGGL((tile_sort_kernel<false, uint32_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n,
-                               p.tb, p.ntiles, (const int*)tstart, (const uint32_t*)at<uint32_t>(ws, p.o_arr), bstart, o);
+                               p.tb, p.ntiles, (const int*)tstart, at<uint32_t>(ws, p.o_arr), bstart, o);
         else
             hipLaunchKernelGGL((tile_sort_kernel<false, uint64_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n,
-                               p.tb, p.ntiles, (const int*)tstart, (const uint64_t*)at<uint64_t>(ws, p.o_arr), bstart, o);
+                               p.tb, p.ntiles, (const int*)tstart, at<uint64_t>(ws, p.o_arr), bstart, o);
         if (p.subset) {
             // the explicit targets through the same tile-level sort: keyed by their atom's
             // bin, ordered by caller position inside a bin -- unless they are exactly
@@ -2007,14 +2046,15 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
             ot.tslot = at<int>(ws, p.o_tslot);
             ot.tsidx = at<int>(ws, p.o_tsidx);
             ot.run_if = listed;
+            ot.stmp = at<void>(ws, p.o_stmp);
             if (narrow)
                 hipLaunchKernelGGL((tile_sort_kernel<true, uint32_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s,
                                    p.nt, p.tb, p.ntiles, (const int*)tstart,
-                                   (const uint32_t*)at<uint32_t>(ws, p.o_tarr), at<int>(ws, p.o_tbstart), ot);
+                                   at<uint32_t>(ws, p.o_tarr), at<int>(ws, p.o_tbstart), ot);
             else
                 hipLaunchKernelGGL((tile_sort_kernel<true, uint64_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s,
                                    p.nt, p.tb, p.ntiles, (const int*)tstart,
-                                   (const uint64_t*)at<uint64_t>(ws, p.o_tarr), at<int>(ws, p.o_tbstart), ot);
+                                   at<uint64_t>(ws, p.o_tarr), at<int>(ws, p.o_tbstart), ot);
         }
         return;
     } else {
@@ -2030,6 +2070,8 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
                        (const uint32_t*)at<uint32_t>(ws, p.o_key),
                        (const uint32_t*)at<uint32_t>(ws, p.o_rank), (const int*)bstart,
                        at<int>(ws, p.o_arr));
+    hipLaunchKernelGGL(sort_big_bins_kernel, dim3(big_bins_grid(p.nbins)), dim3(kSegSortThreads), 0, s, p.nbins,
+                       (const int*)bstart, at<uint32_t>(ws, p.o_arr), at<uint32_t>(ws, p.o_stmp));
     hipLaunchKernelGGL(order_atoms_kernel, dim3(nblocks(p.n)), dim3(256), 0, s, p.n,
                        (const uint32_t*)at<uint32_t>(ws, p.o_key), (const int*)bstart,
                        (const int*)at<int>(ws, p.o_arr), (const float4*)at<float4>(ws, p.o_rec),
@@ -2048,6 +2090,8 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
                            (const uint32_t*)at<uint32_t>(ws, p.o_tkey),
                            (const uint32_t*)at<uint32_t>(ws, p.o_trank), (const int*)tbstart,
                            at<int>(ws, p.o_tslot));
+        hipLaunchKernelGGL(sort_big_bins_kernel, dim3(big_bins_grid(p.nbins)), dim3(kSegSortThreads), 0, s,
+                           p.nbins, (const int*)tbstart, at<uint32_t>(ws, p.o_tslot), at<uint32_t>(ws, p.o_stmp));
         hipLaunchKernelGGL(finish_targets_kernel, dim3(nblocks(p.nbins)), dim3(256), 0, s, p.nbins,
                            p.n, (const int*)tbstart, at<int>(ws, p.o_tslot), target_idx,
                            (const int*)at<int>(ws, p.o_inv), at<int>(ws, p.o_tsidx));

@@ -52,6 +52,7 @@ struct Plan {
     size_t o_arr, o_tor, o_rot;  // o_arr: cell-list ids in arrival order (before the in-bin sort)
     size_t o_tcnt, o_tstart, o_wgb;  // tile-level counting sort: tile totals, starts, chunk bases
     size_t o_tarr;                   // the same sort of explicit targets: their tile buckets
+    size_t o_stmp;                   // segment-sort scratch (8 B per atom or target)
     size_t o_tkey, o_trank, o_tbcnt, o_tbstart, o_tslot, o_tsidx, o_tcaller;
     size_t o_cnt, o_ttot, o_tfix, o_tbase, o_part, o_tot, o_slot;
     int K = 0;              // neighbour slot entries per target
@@ -270,6 +271,9 @@ inline void plan_layout(Plan& p)
     p.o_tarr = take(p.subset ? 8 * nt : 0);
     p.o_tsidx = take(p.subset ? 4 * nt : 0);
     p.o_tcaller = take(p.subset ? 4 * nt : 0);
+    // scratch of the segment sort (tile buckets, bins of the per-bin sort): one entry per
+    // atom or target
+    p.o_stmp = take(8 * std::max(n, nt));
     // per-target counts and slots: one row per target, or per atom when explicit targets
     // turn out to be the atoms 0 .. nt - 1 (the count then runs over every atom of a tile)
     // (rows padded to 256 targets: the group rows of a row length of 2 mod 4 targets, e.g.
