@@ -8,6 +8,7 @@ namespace dg {
 constexpr int kScanBlock = 256;
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kScanBlock * kScanItems;  // 2048 items per workgroup
+constexpr int kSmallScanBlock = 1024;  // the one-workgroup scan of short arrays
 
 // Inclusive scan across one wave64.
 template <typename T>
@@ -134,13 +135,13 @@ inline void device_excl_scan(const Tin* in, int64_t n, Tout* out, Tout* part, hi
 // Exclusive scan of in[0..n) into out[0..n] (out[n] = sum) by one workgroup, for short
 // arrays (one launch instead of three); the sum is also stored to *sum_out if given.
 template <typename Tin, typename Tout>
-__global__ __launch_bounds__(kScanBlock) void small_scan_kernel(const Tin* __restrict__ in,
-                                                                int64_t n, Tout* __restrict__ out,
-                                                                int64_t* __restrict__ sum_out)
+__global__ __launch_bounds__(kSmallScanBlock) void small_scan_kernel(const Tin* __restrict__ in,
+                                                                     int64_t n, Tout* __restrict__ out,
+                                                                     int64_t* __restrict__ sum_out)
 {
-    __shared__ Tout s_w[kScanBlock / 64];
+    __shared__ Tout s_w[kSmallScanBlock / 64];
     Tout carry = 0;
-    for (int64_t b0 = 0; b0 < n; b0 += kScanTile) {
+    for (int64_t b0 = 0; b0 < n; b0 += kSmallScanBlock * kScanItems) {
         const int64_t base = b0 + (int64_t)threadIdx.x * kScanItems;
         Tout v[kScanItems], sum = 0;
 #pragma unroll
@@ -149,7 +150,7 @@ __global__ __launch_bounds__(kScanBlock) void small_scan_kernel(const Tin* __res
             sum += v[k];
         }
         Tout tot;
-        Tout ex = block_excl_scan<Tout, kScanBlock>(sum, s_w, &tot) + carry;
+        Tout ex = block_excl_scan<Tout, kSmallScanBlock>(sum, s_w, &tot) + carry;
 #pragma unroll
         for (int k = 0; k < kScanItems; ++k) {
             if (base + k < n) out[base + k] = ex;
@@ -169,7 +170,7 @@ __global__ void copy_sum_kernel(const Tout* __restrict__ src, int64_t* __restric
     if (threadIdx.x == 0 && blockIdx.x == 0) *dst = (int64_t)*src;
 }
 
-constexpr int64_t kSmallScanMax = 8192;  // one workgroup takes ~2.4 us per 2048 items
+constexpr int64_t kSmallScanMax = 8192;  // one pass of the 1024-thread workgroup
 
 // Exclusive scan choosing the one-workgroup kernel for short arrays (it beats three
 // launches up to a few thousand items).
@@ -178,7 +179,7 @@ inline void excl_scan(const Tin* in, int64_t n, Tout* out, Tout* part, hipStream
                       int64_t* sum_out = nullptr)
 {
     if (n <= kSmallScanMax) {
-        hipLaunchKernelGGL((small_scan_kernel<Tin, Tout>), dim3(1), dim3(kScanBlock), 0, s, in, n,
+        hipLaunchKernelGGL((small_scan_kernel<Tin, Tout>), dim3(1), dim3(kSmallScanBlock), 0, s, in, n,
                            out, sum_out);
         return;
     }
