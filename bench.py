@@ -249,7 +249,7 @@ def cpu_baseline(args, box, n, E_gpu):
     """The C oracle (the reference algorithm with the canonical predicate) on this host:
     the full build with all the threads the job may use, median of 3; a one-thread run on
     a bounded sample (every 10th atom as a target, the ``radius_graph_pbc_ex`` path), median
-    of 3; and the Morton SFC keys of all atoms (one thread), median of 5."""
+    of 3; and the Morton SFC keys of all atoms, with all threads and with one, median of 5."""
     import numpy as np
 
     import oracle
@@ -279,7 +279,9 @@ def cpu_baseline(args, box, n, E_gpu):
                                                   target_indices=sample_t, threads=1), 3)
     E_one = len(oc["src"])
     del oc
-    keys_s, _ = timed(lambda: oracle.morton_keys(box.pos.astype(np.float32)), 5)
+    p32 = box.pos.astype(np.float32)
+    keys_s, _ = timed(lambda: oracle.morton_keys(p32, threads=thr), 5)
+    keys1_s, _ = timed(lambda: oracle.morton_keys(p32, threads=1), 5)
     cpu = {"value": round(E_cpu / full_s / 1e9, 5), "unit": "Gedges/s", "cores": thr,
            "kind": "port",
            "sample": f"full build of {args.config} ({n} atoms, {E_cpu} edges) by the C oracle "
@@ -292,8 +294,8 @@ def cpu_baseline(args, box, n, E_gpu):
                           "sample": f"every 10th atom as a target ({len(sample_t)} targets, {E_one} "
                                     f"edges), median of 3: {one_s * 1e3:.0f} ms",
                           "ms_per_rebuild_extrapolated": round(one_s * E_cpu / max(E_one, 1) * 1e3, 1)},
-           "sfc_keys": {"ms": round(keys_s * 1e3, 2), "cores": 1,
-                        "sample": f"Morton keys of all {n} atoms, median of 5"}}
+           "sfc_keys": {"ms": round(keys_s * 1e3, 2), "cores": thr, "ms_one_thread": round(keys1_s * 1e3, 2),
+                        "sample": f"Morton keys of all {n} atoms, median of 5 each"}}
     if E_cpu != E_gpu:
         cpu["edge_count_mismatch"] = [E_cpu, E_gpu]
     return cpu

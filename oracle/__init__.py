@@ -70,7 +70,7 @@ def lib():
         L.orc_ref32_decide.restype = None
         L.orc_ref32_decide.argtypes = [_p, _i64, _p, _p, _dbl, _i64, _p, _p, _p, _p]
         L.orc_sfc_bounds.argtypes = [_p, _i64, _p, _p]
-        L.orc_morton_keys.argtypes = [_p, _i64, _p, _p, _p]
+        L.orc_morton_keys.argtypes = [_p, _i64, _p, _p, _p, ctypes.c_int]
         L.orc_hilbert_keys.argtypes = [_p, _i64, _p, _p, _p]
         L.orc_sfc_labels.argtypes = [_p, _i64, _i64, _p, _p]
         _lib = L
@@ -229,14 +229,14 @@ def sfc_bounds(pos):
     return mn, rg
 
 
-def morton_keys(pos, mn=None, rg=None):
+def morton_keys(pos, mn=None, rg=None, threads=1):
     L = lib()
     pos = np.ascontiguousarray(pos, np.float32)
     if mn is None:
         mn, rg = sfc_bounds(pos)
     keys = np.empty(pos.shape[0], np.int64)
     L.orc_morton_keys(_ptr(pos), pos.shape[0], _ptr(np.ascontiguousarray(mn, np.float32)),
-                      _ptr(np.ascontiguousarray(rg, np.float32)), _ptr(keys))
+                      _ptr(np.ascontiguousarray(rg, np.float32)), _ptr(keys), int(threads))
     return keys
 
 

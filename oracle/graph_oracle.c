@@ -538,9 +538,13 @@ void orc_sfc_bounds(const float* pos, int64_t n, float* mn, float* range)
     }
 }
 
-void orc_morton_keys(const float* pos, int64_t n, const float* mn, const float* range, int64_t* keys)
+/* threads > 0: that many OpenMP threads (each atom's key is independent of the others) */
+void orc_morton_keys(const float* pos, int64_t n, const float* mn, const float* range, int64_t* keys,
+                     int threads)
 {
     const uint32_t gmax = (1u << 21) - 1;
+    const int nthr = threads > 0 ? threads : omp_get_max_threads();
+#pragma omp parallel for schedule(static) num_threads(nthr)
     for (int64_t i = 0; i < n; i++) {
         uint32_t q[3];
         for (int a = 0; a < 3; a++) {
