@@ -528,9 +528,11 @@ __global__ __launch_bounds__(kF1Threads) void filter1_kernel(const void* __restr
         if (keep[k]) {
             const int64_t q = o + (int64_t)fk;
             const int64_t e = e0 + kF1Threads * k;
-            osrc[q] = s[k];
-            odst[q] = d[k];
-            for (int c = 0; c < 3; ++c) osh[3 * q + c] = sh[3 * e + c];
+            // non-temporal: the output stream stays out of the caches the gathers use
+            // (C3: 2.05 -> 1.99 ms)
+            __builtin_nontemporal_store(s[k], &osrc[q]);
+            __builtin_nontemporal_store(d[k], &odst[q]);
+            for (int c = 0; c < 3; ++c) __builtin_nontemporal_store(sh[3 * e + c], &osh[3 * q + c]);
         }
         o += (int64_t)((tot[k >> 2] >> (16 * (k & 3))) & 0xFFFFu);
     }
