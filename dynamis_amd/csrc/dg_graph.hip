@@ -1569,6 +1569,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         if (MODE == 0 && threadIdx.x == 0) {
             a.ttot[ord] = (int)tt;
             a.tfix[ord] = fix;
+            if (fix) atomicOr((unsigned long long*)&a.totals[3], 1ull);  // the fix-up pass has work
         }
     }
     return out;
@@ -1616,7 +1617,9 @@ __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
             FixLds f;
             Expand2Lds e;
         } u;
-        // a grid of at most DG_FIXGRID workgroups walks the tiles: most have nothing to do
+        // a grid of at most DG_FIXGRID workgroups walks the tiles: most have nothing to do,
+        // and in most builds no tile has (the count pass raises totals[3] when one does)
+        if (a.totals[3] == 0) return;
         for (int64_t ord = blockIdx.x; ord < a.ntiles; ord += gridDim.x) {
             const int fix = a.tfix[ord];
             if (fix == 0) continue;

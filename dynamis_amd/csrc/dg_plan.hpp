@@ -247,6 +247,8 @@ inline void plan_layout(Plan& p)
     auto take = [&](size_t bytes) { size_t r = o; o = align_up(o + (bytes ? bytes : 1)); return r; };
     const size_t n = (size_t)p.n, nt = (size_t)p.nt, nbins = (size_t)p.nbins;
     const size_t ntl = (size_t)p.ntiles;
+    // the build's totals: [0] edges, [1] status flags, [2] explicit targets that are not
+    // 0 .. nt - 1, [3] some tile needs the fix-up pass; cleared at the start of a build
     p.o_tot = take(8 * 8);
     p.o_key = take(4 * n);
     p.o_rank = take(4 * n);
