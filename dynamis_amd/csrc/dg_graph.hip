@@ -382,12 +382,8 @@ constexpr int kTileSortCap = 2048;  // bucket entries ordered in LDS (larger: ar
 constexpr int kTileSortPer = kTileSortCap / 256;
 struct TileSortLds {
     union {
-        struct {
-            int id[kTileSortCap];
-            int lb[kTileSortCap];
-            int by[kTileSortCap];  // ids grouped by bin
-        };
-        SegSortLds seg;  // a larger bucket: sorted in global memory
+        int by[kTileSortCap];  // ids grouped by bin
+        SegSortLds seg;        // a larger bucket: sorted in global memory
     };
     int cnt[kTileMax * kTileMax * kTileMax];
     int st[kTileMax * kTileMax * kTileMax + 1];
@@ -449,8 +445,6 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
             qi[u] = bk_id(w);
             ql[u] = bk_bin(w);
             q[u] = gather(qi[u]);
-            S.id[e] = qi[u];
-            S.lb[e] = ql[u];
             atomicAdd(&S.cnt[ql[u]], 1);
         }
     }
