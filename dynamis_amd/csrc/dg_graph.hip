@@ -453,10 +453,10 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
     __syncthreads();
     // bin starts inside the bucket (tb <= 216: one pass of a 256-thread scan)
     {
-        const int c = threadIdx.x < tb ? S.cnt[threadIdx.x] : 0;
+        const int c = (int)threadIdx.x < tb ? S.cnt[threadIdx.x] : 0;
         int tot;
         const int ex = block_excl_scan<int, 256>(c, S.w32, &tot);
-        if (threadIdx.x < tb) {
+        if ((int)threadIdx.x < tb) {
             S.st[threadIdx.x] = ex;
             S.cnt[threadIdx.x] = ex;  // placement cursors
             bstart[r * tb + threadIdx.x] = base + ex;
@@ -916,7 +916,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
     for (int k0 = 0; k0 < ntg; k0 += kBlock) {
         const int nbatch = min(kBlock, ntg - k0);
         const int j = tbeg + k0 + threadIdx.x;
-        const bool active = threadIdx.x < nbatch;
+        const bool active = (int)threadIdx.x < nbatch;
         const int mycnt = active ? a.cnt[j] : 0;
         int btot;
         const int ex = block_excl_scan<int, kBlock>(mycnt, sh.w32, &btot);
@@ -1275,7 +1275,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         const int nbatch = min(kBlock, ntg - k0);
         const int kk = k0 + threadIdx.x;
         const int j = tbeg + kk;
-        const bool in_batch = threadIdx.x < nbatch;
+        const bool in_batch = (int)threadIdx.x < nbatch;
         bool active = in_batch;
 
         // ---- per-lane target state

@@ -51,7 +51,7 @@ __global__ void bounds_partial_kernel(const float* __restrict__ pos, int64_t n,
     for (int a = 0; a < 3; ++a) { s_mn[a][threadIdx.x] = mn[a]; s_mx[a][threadIdx.x] = mx[a]; }
     __syncthreads();
     for (int o = 128; o > 0; o >>= 1) {
-        if (threadIdx.x < o)
+        if ((int)threadIdx.x < o)
             for (int a = 0; a < 3; ++a) {
                 s_mn[a][threadIdx.x] = fminf(s_mn[a][threadIdx.x], s_mn[a][threadIdx.x + o]);
                 s_mx[a][threadIdx.x] = fmaxf(s_mx[a][threadIdx.x], s_mx[a][threadIdx.x + o]);
