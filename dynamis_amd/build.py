@@ -35,6 +35,7 @@ FLAGS = [
     "-Xclang", "-target-feature", "-Xclang", "-packed-fp32-ops",
     "-I" + os.path.join(ROOT, "include"),
     "-Wall",
+    "-Wextra",
 ]
 
 
