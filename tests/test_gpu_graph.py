@@ -380,12 +380,11 @@ def test_filter_edges_to_radius(cuda, dtype):
 
 
 def test_filter_large_list(cuda):
-    """More than 2.1M edges: the per-block kept counts (one per 256 edges) exceed one
-    workgroup's scan, so the multi-kernel device scan produces the block offsets; the last
-    block is partial."""
+    """More than 2.1M edges: hundreds of look-back tiles of 4096 edges (offsets passed
+    through many predecessors' status words), the last tile partial."""
     _announce("filter, large list")
     E = _filter_case(cuda, 30000, 18, 6.5, 6.0, torch.float32)
-    assert E > 2_100_000 and E % 256 != 0
+    assert E > 2_100_000 and E % 4096 != 0
 
 
 def test_filter_rejects_out_of_range_atoms(cuda):
