@@ -121,7 +121,7 @@ dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64
  * outputs in the same order), with the workspace taken from a static device array inside
  * the library (64 MiB per GPU, held until the process ends) instead of a caller buffer;
  * it calls no hipMalloc / hipFree.  Builds whose dg_graph_workspace_size() exceeds
- * 64 MiB (about 150k atoms at 0.1 atoms/A^3 and r = 6 A) are refused with
+ * 64 MiB (about 140k atoms at 0.1 atoms/A^3 and r = 6 A) are refused with
  * DG_ERR_WORKSPACE.  The edge count and status flags are copied on the stream to
  *   totals_out   device int64 [2]: {total_edges, flags (DG_FLAG_*)}
  * which the caller reads when it needs them (an edge count above `capacity`, or
