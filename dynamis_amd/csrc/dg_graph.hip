@@ -378,7 +378,7 @@ __global__ __launch_bounds__(1024) void tile_scatter_kernel(int64_t n, int tb, i
     }
 }
 
-constexpr int kTileSortCap = 2048;  // bucket entries ordered in LDS (larger: arrival order in bins)
+constexpr int kTileSortCap = 2048;  // bucket entries ordered in LDS (larger: sorted by segment_sort)
 constexpr int kTileSortPer = kTileSortCap / 256;
 struct TileSortLds {
     union {
