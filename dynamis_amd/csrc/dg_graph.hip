@@ -941,7 +941,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
         }
         const int64_t wbase = ebase + E0;
         const char* __restrict__ sl = (const char*)a.slot + (size_t)16 * (tbeg + k0);
-        const uint32_t gstep = 16u * (uint32_t)a.nslot;  // bytes between a target's groups
+        const uint64_t gstep = 16ull * (uint64_t)a.nslot;  // bytes between a target's groups
 
         // Edges [b0, b1) of the batch (b1 - b0 <= 64 * kExpandIlp), lane-strided: edge
         // b0 + 64u + lane -> source id, target id, packed shift; ok = false past b1 or for
@@ -971,9 +971,9 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
             }
 #pragma unroll
             for (int u = 0; u < kExpandIlp; ++u) {
-                const uint32_t at = L.kk[u] < a.K ? (uint32_t)(L.kk[u] >> 3) * gstep +
-                                                        16u * (uint32_t)L.tt[u] + 2u * (L.kk[u] & 7)
-                                                  : 0u;
+                const uint64_t at = L.kk[u] < a.K ? (uint64_t)(uint32_t)(L.kk[u] >> 3) * gstep +
+                                                        (16u * (uint32_t)L.tt[u] + 2u * (L.kk[u] & 7))
+                                                  : 0ull;
                 L.raw[u] = (int)*(const uint16_t*)(sl + at);
             }
             // the lane holding edge b1 - 1 has its target in t
@@ -1451,8 +1451,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             char* const lbb = lb0 + lane_off;
             const bool slots = slotted;
             char* const slotb = (char*)a.slot;
-            const uint32_t gstep = 16u * (uint32_t)a.nslot;  // bytes between a target's groups
-            uint32_t goff = 16u * (uint32_t)j;                // byte offset of group kf2 / 16
+            const uint64_t gstep = 16ull * (uint64_t)a.nslot;  // bytes between a target's groups
+            uint64_t goff = 16ull * (uint64_t)j;                // byte offset of group kf2 / 16
             int kf2 = 0;                                      // 2 x entries stored (or skipped)
             int klim = 2 * kRing - 4;                         // kf2 + 28: the in-row flush mark
             const int K2 = 2 * a.K;
@@ -1911,7 +1911,7 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     // slot rows: one per target, or per atom when the targets are the atoms with ids < nt
     // (every atom of a tile is then a lane)
     const int64_t nrow = p.nrow;
-    a.slot = 2.0 * p.K * (double)nrow < 4294967296.0 ? at<uint16_t>(ws, p.o_slot) : nullptr;
+    a.slot = at<uint16_t>(ws, p.o_slot);
     a.K = p.K;
     a.nslot = nrow;
     a.ntarg = p.nt;

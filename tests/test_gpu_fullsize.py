@@ -10,8 +10,8 @@ Cases: the headline C3 box (1M atoms, ~9.05e7 edges); C4 at its stated 500k atom
 triclinic cell scaled by 1.3934); the C5 random walk of the benchmark (degrees at full
 size on frames 1, 50 and 99; every edge on a reduced box over 10 frames); and the sort
 paths no benchmark configuration reaches: more tiles than the tile-level sort takes (the
-per-bin fallback), with more than 2^24 atoms, and 64-bit tile-bucket entries (more than
-2^24 targets).
+per-bin fallback), with more than 2^24 atoms, 64-bit tile-bucket entries (more than
+2^24 targets), and a slot array past 4 GiB (64-bit slot addresses).
 """
 import itertools
 
@@ -176,3 +176,39 @@ def test_more_than_2_24_targets(cuda):
                                           torch.from_numpy(tg).to(cuda))
     deg, _ = oracle.radius_graph_counts(box.pos, _cell_used(box), box.pbc, box.radius)
     assert np.array_equal(cnt.cpu().numpy(), deg[tg])
+
+
+def test_slots_past_4_gib(cuda):
+    """12M atoms at C3's density and radius (1.09e9 edges): the count pass's slot array
+    (2 bytes x 184 entries x 12M targets) is larger than 4 GiB, so slot addresses need 64
+    bits.  Checks without the oracle (whose run would take minutes here): the written edges
+    have exactly the degrees the count pass reports, each satisfies the predicate (fp64,
+    canonical form), none appears twice, and the set is symmetric under
+    (i, j, S) <-> (j, i, -S)."""
+    n = 12_000_000
+    box = configs.uniform(n, density=0.1, seed=45, dtype=np.float32)
+    _announce(f"N={n}: slots past 4 GiB")
+    p = torch.from_numpy(box.pos).to(cuda)
+    c = torch.from_numpy(box.cell)
+    b = torch.tensor([True] * 3)
+    assert 2 * 184 * n > 2 ** 32
+    ei, co, nn, cnt = impl.radius_graph_pbc_ex(p, c, b, box.radius, 0, False)
+    E = ei.shape[1]
+    assert E > 1.0e9 and int(nn.item()) == E
+    assert torch.equal(torch.bincount(ei[1], minlength=n).to(torch.int32), cnt)
+    cell = torch.from_numpy(np.asarray(box.cell, np.float32).astype(np.float64)).to(cuda)
+    p64 = p.double()
+    r2 = float(np.float32(box.radius)) ** 2
+    step = 100_000_000
+    for e0 in range(0, E, step):
+        s_, d_ = ei[0, e0:e0 + step], ei[1, e0:e0 + step]
+        v = p64[s_] + co[e0:e0 + step].double() @ cell - p64[d_]
+        d2 = (v * v).sum(1)
+        assert bool((d2 <= r2 * (1 + 1e-12)).all()) and bool((d2 > 1e-8).all())
+        del v, d2
+    nb, sb = _layout(n, 1)
+    S = co.to(torch.int64)
+    fwd = torch.sort(_keys_torch(ei[0], ei[1], S, nb, sb)).values
+    assert bool((fwd[1:] > fwd[:-1]).all())  # no edge twice
+    rev = torch.sort(_keys_torch(ei[1], ei[0], -S, nb, sb)).values
+    assert torch.equal(fwd, rev)
