@@ -63,11 +63,13 @@ Layout layout(int64_t n, int64_t W)
     L.o_rflag = take((size_t)n);
     L.o_g2l = take(4 * (size_t)n);
     L.o_pid = take(2 * (size_t)n);
-    L.o_hs = take(4 * nh);
-    L.o_hr = take(4 * nh);
-    L.o_os = take(8 * (nh + 1));
-    L.o_or = take(8 * (nh + 1));
-    L.o_part = take(8 * (nh / kScanTile + 2));
+    // the send and receive histograms side by side, scanned as one array: the receive
+    // offsets then carry the send total, which their readers subtract
+    L.o_hs = take(4 * 2 * nh);
+    L.o_hr = L.o_hs + 4 * nh;
+    L.o_os = take(8 * (2 * nh + 1));
+    L.o_or = L.o_os + 8 * nh;
+    L.o_part = take(8 * (2 * nh / kScanTile + 2));
     L.total = o;
     return L;
 }
@@ -219,6 +221,9 @@ __global__ __launch_bounds__(256) void walk_kernel(Args A, int* __restrict__ his
     if (u >= A.nu) return;  // whole wave; no workgroup barrier below
     for (int p = lane; p < A.W; p += 64) run[p] = 0;
     const unsigned long long lt = (1ull << lane) - 1ull;
+    // the receive offsets come from one scan with the send histogram in front, so they
+    // carry the send total, which is their first entry
+    const int64_t base = MODE == 1 && RECV ? off[0] : 0;
     const int64_t a0 = u * kUnit;
     for (int st = 0; st < kUnit && a0 + st < A.n; st += 64) {
         const int64_t a = a0 + st + lane;
@@ -235,7 +240,7 @@ __global__ __launch_bounds__(256) void walk_kernel(Args A, int* __restrict__ his
                 const int c = __popcll(bal);
                 const int r = run[p];
                 if (MODE == 1 && has) {
-                    const int64_t pos = off[(int64_t)p * A.nu + u] + r + __popcll(bal & lt);
+                    const int64_t pos = off[(int64_t)p * A.nu + u] - base + r + __popcll(bal & lt);
                     if (RECV) {
                         out0[pos] = a;                  // recv_atom_global
                         out1[pos] = A.num_local + pos;  // recv_ghost_indices
@@ -257,11 +262,12 @@ __global__ void offsets_kernel(const int64_t* __restrict__ os, const int64_t* __
 {
     const int64_t p = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
     if (p > W) return;
+    // (orr follows os in one scan: its entries carry the send total, orr[0])
     send_off[p] = os[p * nu];
-    recv_off[p] = orr[p * nu];
+    recv_off[p] = orr[p * nu] - orr[0];
     if (p == W) {
         tot[0] = os[W * nu];
-        tot[1] = orr[W * nu];
+        tot[1] = orr[W * nu] - orr[0];
     }
 }
 
@@ -358,8 +364,7 @@ dg_status dg_halo_count(const dg_halo_desc* d, const int64_t* src, const int64_t
                            (const int64_t*)nullptr, (int64_t*)nullptr, (int64_t*)nullptr);
     }
     const int64_t nh = L.W * L.nu;
-    device_excl_scan<int, int64_t>(hs, nh, os, part, s);
-    device_excl_scan<int, int64_t>(hr, nh, orr, part, s);
+    device_excl_scan<int, int64_t>(hs, 2 * nh, os, part, s);  // hs, hr side by side
     hipLaunchKernelGGL(offsets_kernel, dim3(nblk(L.W + 1)), dim3(256), 0, s, (const int64_t*)os,
                        (const int64_t*)orr, L.W, L.nu, send_offsets, recv_offsets, tot);
     return launch_ok("dg_halo_count");
