@@ -65,19 +65,34 @@ __global__ void bounds_partial_kernel(const float* __restrict__ pos, int64_t n,
         }
 }
 
-__global__ void bounds_final_kernel(const float* __restrict__ part, int nb, float* __restrict__ out)
+// One workgroup of 256 threads folds the nb <= 1024 partial bounds (min and max are exact,
+// so the result does not depend on the order).
+__global__ __launch_bounds__(256) void bounds_final_kernel(const float* __restrict__ part, int nb,
+                                                           float* __restrict__ out)
 {
-    if (threadIdx.x != 0) return;
-    for (int a = 0; a < 3; ++a) {
-        float mn = INFINITY, mx = -INFINITY;
-        for (int b = 0; b < nb; ++b) {
-            mn = fminf(mn, part[6 * b + a]);
-            mx = fmaxf(mx, part[6 * b + 3 + a]);
+    __shared__ float s_mn[3][256], s_mx[3][256];
+    float mn[3] = {INFINITY, INFINITY, INFINITY}, mx[3] = {-INFINITY, -INFINITY, -INFINITY};
+    for (int b = threadIdx.x; b < nb; b += 256)
+        for (int a = 0; a < 3; ++a) {
+            mn[a] = fminf(mn[a], part[6 * b + a]);
+            mx[a] = fmaxf(mx[a], part[6 * b + 3 + a]);
         }
-        float rg = mx - mn;
-        out[a] = mn;
-        out[3 + a] = rg > 0.0f ? rg : 1.0f;
+    for (int a = 0; a < 3; ++a) { s_mn[a][threadIdx.x] = mn[a]; s_mx[a][threadIdx.x] = mx[a]; }
+    __syncthreads();
+    for (int o = 128; o > 0; o >>= 1) {
+        if ((int)threadIdx.x < o)
+            for (int a = 0; a < 3; ++a) {
+                s_mn[a][threadIdx.x] = fminf(s_mn[a][threadIdx.x], s_mn[a][threadIdx.x + o]);
+                s_mx[a][threadIdx.x] = fmaxf(s_mx[a][threadIdx.x], s_mx[a][threadIdx.x + o]);
+            }
+        __syncthreads();
     }
+    if (threadIdx.x == 0)
+        for (int a = 0; a < 3; ++a) {
+            const float rg = s_mx[a][0] - s_mn[a][0];
+            out[a] = s_mn[a][0];
+            out[3 + a] = rg > 0.0f ? rg : 1.0f;
+        }
 }
 
 // ------------------------------------------------------------------ keys
@@ -143,8 +158,15 @@ __global__ void key_span_kernel(const int64_t* __restrict__ keys, int64_t n,
         o |= k;
         a &= k;
     }
-    atomicOr(&span[0], o);
-    atomicAnd(&span[1], a);
+    // fold the wave's values first: one pair of device atomics per wave, not per thread
+    for (int m = 32; m > 0; m >>= 1) {
+        o |= (unsigned long long)__shfl_xor((long long)o, m, 64);
+        a &= (unsigned long long)__shfl_xor((long long)a, m, 64);
+    }
+    if ((threadIdx.x & 63) == 0) {
+        atomicOr(&span[0], o);
+        atomicAnd(&span[1], a);
+    }
 }
 
 __global__ void span_init_kernel(unsigned long long* span)
@@ -624,7 +646,7 @@ dg_status dg_sfc_keys(const float* pos, int64_t n, int32_t curve, int64_t* keys,
     int nb = (int)((n + 255) / 256);
     if (nb > 1024) nb = 1024;
     hipLaunchKernelGGL(bounds_partial_kernel, dim3(nb), dim3(256), 0, s, pos, n, part);
-    hipLaunchKernelGGL(bounds_final_kernel, dim3(1), dim3(64), 0, s, (const float*)part, nb, bnd);
+    hipLaunchKernelGGL(bounds_final_kernel, dim3(1), dim3(256), 0, s, (const float*)part, nb, bnd);
     hipLaunchKernelGGL(keys_kernel, dim3(nblk(n)), dim3(256), 0, s, pos, n, (int)curve,
                        (const float*)bnd, keys);
     return launch_ok("dg_sfc_keys");
