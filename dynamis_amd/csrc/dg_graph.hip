@@ -65,6 +65,14 @@ dg_status fail(dg_status st, const std::string& msg)
 constexpr int kRegPerThread = (kMaxRegion + kBlock - 1) / kBlock;
 constexpr int kBinSortMax = 128;
 constexpr int kExpandIlp = 4;  // 64-edge steps per iteration of the expansion (even)
+
+// Whether a device-wide flag word still reads 0 (a device-scope load, so a flag another
+// XCD set is seen): raising flags only then keeps the atomics on one address few.
+__device__ __forceinline__ bool flag_clear(int64_t* w)
+{
+    return __hip_atomic_load(w, __ATOMIC_RELAXED, __HIP_MEMORY_SCOPE_AGENT) == 0;
+}
+
 // search_kernel<1> work of a tile, set by the count pass
 constexpr int kFixOver = 1;     // a target has more than K neighbours
 constexpr int kFixChunked = 2;  // the region needs more than two LDS chunks (or no slots)
@@ -534,7 +542,10 @@ __global__ void target_prefix_kernel(int64_t nt, int64_t n, const int64_t* __res
     bool other = nt > n;
     for (int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; t < nt && !other; t += stride)
         other = tgt[t] != t;
-    if (__builtin_amdgcn_ballot_w64(other) != 0ull && (threadIdx.x & 63) == 0)
+    // one device atomic per workgroup at most, and none once the flag is seen set (atomics
+    // on one address serialise: one per wave of a large list costs tens of microseconds)
+    __shared__ int s_w[256 / 64];
+    if (block_any<256>(other, s_w) && threadIdx.x == 0 && flag_clear(&totals[2]))
         atomicOr((unsigned long long*)&totals[2], 1ull);
 }
 
@@ -1563,7 +1574,8 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         if (MODE == 0 && threadIdx.x == 0) {
             a.ttot[ord] = (int)tt;
             a.tfix[ord] = fix;
-            if (fix) atomicOr((unsigned long long*)&a.totals[3], 1ull);  // the fix-up pass has work
+            if (fix && flag_clear(&a.totals[3]))  // the fix-up pass has work
+                atomicOr((unsigned long long*)&a.totals[3], 1ull);
         }
     }
     return out;
