@@ -1711,10 +1711,13 @@ __global__ void brute_kernel(BruteArgs a)
         int fs[3];
         load_pos(a.pos, a.f64, j, ps);
         brute_floor(a, ps, fs);
+        // an edge's shift is its periodic image plus the floor difference of the two atoms
+        // (radius_graph_kernels.cu:282-303): images |I_d| <= kimg_d around ft - fs
         int lo[3], hi[3];
         for (int d = 0; d < 3; ++d) {
-            if (a.pbc[d]) { lo[d] = -a.kimg[d]; hi[d] = a.kimg[d]; }
-            else { lo[d] = hi[d] = ft[d] - fs[d]; }
+            const int df = ft[d] - fs[d];
+            if (a.pbc[d]) { lo[d] = df - a.kimg[d]; hi[d] = df + a.kimg[d]; }
+            else { lo[d] = hi[d] = df; }
         }
         for (int s0 = lo[0]; s0 <= hi[0]; ++s0)
             for (int s1 = lo[1]; s1 <= hi[1]; ++s1)

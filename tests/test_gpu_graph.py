@@ -225,6 +225,18 @@ def test_all_pairs_fallback(cuda):
     check_parity(pos, cell, (1, 0, 1), 10.0, cuda, name="all-pairs partial")
 
 
+def test_all_pairs_far_positions(cuda):
+    """The all-pairs kernel with atoms up to three cell lengths outside the cell: an edge's
+    shift is its image plus the difference of the two atoms' floors, so the image range
+    must be taken around that difference (cubic and triclinic, full and partial PBC)."""
+    pos, cell = _rand(12, 3.0, 34, lo=-3.0, hi=4.0)
+    check_parity(pos, cell, (1, 1, 1), 13.0, cuda, name="all-pairs far positions")
+    check_parity(pos, cell, (1, 0, 1), 13.0, cuda, name="all-pairs far positions partial")
+    tri = np.array([[3.0, 0.0, 0.0], [0.8, 2.8, 0.0], [-0.5, 0.4, 3.1]])
+    pos, _ = _rand(10, 1.0, 35, dtype=np.float64, lo=-2.5, hi=3.5, cell=tri)
+    check_parity(pos, tri, (1, 1, 0), 13.0, cuda, name="all-pairs far positions triclinic")
+
+
 def test_all_pairs_fallback_many_atoms(cuda):
     """The all-pairs kernel (a stencil of more than 768 bins: r > 4 cell widths) on tens of
     atoms with tens of thousands of periodic-image neighbours each, orthorhombic and

@@ -66,3 +66,43 @@ def test_random_case(cuda, seed):
     want = oracle.canonical_sort(o["src"], o["dst"], o["shift"])
     for a, b in zip(got, want):
         assert np.array_equal(a, b)
+
+
+def _brute_case(seed):
+    """Cells much smaller than the radius (the all-pairs kernel): r = 4.5 - 7 times the
+    thinnest cell width, positions inside or up to three cells outside the cell."""
+    rng = np.random.default_rng(5000 + seed)
+    L = rng.uniform(2.0, 5.0)
+    cell = np.eye(3) * L
+    if seed % 3 == 1:
+        cell[1, 0], cell[2, 0], cell[2, 1] = rng.uniform(-0.3, 0.3, 3) * L
+    elif seed % 3 == 2:
+        cell = cell + rng.uniform(-0.25, 0.25, (3, 3)) * L
+    vol = abs(np.linalg.det(cell))
+    dmin = vol / max(np.linalg.norm(np.cross(cell[1], cell[2])), np.linalg.norm(np.cross(cell[2], cell[0])),
+                     np.linalg.norm(np.cross(cell[0], cell[1])))
+    r = float(rng.uniform(4.5, 7.0) * dmin)
+    n = int(rng.integers(1, 40))
+    pbc = (True, True, True) if seed % 2 else tuple(bool(b) for b in rng.integers(0, 2, 3))
+    lo, hi = (0.0, 1.0) if seed % 4 == 0 else (-3.0, 4.0)
+    pos = (rng.uniform(lo, hi, (n, 3)) @ cell).astype(np.float64 if seed % 2 else np.float32)
+    tg = rng.integers(0, n, max(1, n // 2)).astype(np.int64) if seed % 5 == 4 else None
+    return cell, pbc, r, pos, tg
+
+
+@pytest.mark.parametrize("seed", range(24))
+def test_random_all_pairs(cuda, seed):
+    cell, pbc, r, pos, tg = _brute_case(seed)
+    print(f"\n[case] random all-pairs seed={seed} n={len(pos)} dtype={pos.dtype} pbc={pbc} r={r:.3f} "
+          f"targets={None if tg is None else len(tg)}", flush=True)
+    pt = torch.from_numpy(np.ascontiguousarray(pos)).to(cuda)
+    tt = None if tg is None else torch.from_numpy(tg).to(cuda)
+    ei, co, nn, cnt = impl.radius_graph_pbc_ex(pt, torch.from_numpy(cell), torch.tensor(pbc), r, 0, False, tt)
+    cell_used = np.asarray(cell, np.float64).astype(pos.dtype).astype(np.float64)
+    o = oracle.radius_graph(pos, cell_used, pbc, float(np.float32(r)), target_indices=tg)
+    assert ei.shape[1] == len(o["src"]) == int(nn.item())
+    assert np.array_equal(cnt.cpu().numpy(), o["counts"])
+    got = oracle.canonical_sort(ei[0].cpu().numpy(), ei[1].cpu().numpy(), co.cpu().numpy().astype(np.int64))
+    want = oracle.canonical_sort(o["src"], o["dst"], o["shift"])
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b)
