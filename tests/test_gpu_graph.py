@@ -552,3 +552,43 @@ def test_dense_cube_in_sparse_box(cuda, side, cube, rho_bg, rho_c):
     cl = rng.uniform(0, cube, (int(rho_c * cube ** 3), 3)) + (side - cube) / 2
     pos = np.concatenate([bg, cl]).astype(np.float32)
     check_parity(pos, np.eye(3) * side, (1, 1, 1), 5.0, cuda, name=f"dense cube {cube} in {side}")
+
+
+@pytest.mark.parametrize("which", ["left-handed", "negative diagonal", "permuted rows", "tiny skewed"])
+def test_unusual_cells(cuda, which):
+    """Cells the lower-triangular fast path does not take: a left-handed cell (negative
+    determinant), a diagonal with negative entries, the rows of a triclinic cell permuted,
+    and a strongly skewed small cell (all-pairs range); parity with the oracle, full and
+    partial PBC, atoms inside and outside the cell."""
+    base = np.array([[14.0, 0.0, 0.0], [3.0, 13.0, 0.0], [-2.0, 1.5, 12.0]])
+    r = 5.0
+    if which == "left-handed":
+        cell = base.copy()
+        cell[2] *= -1.0
+    elif which == "negative diagonal":
+        cell = np.diag([-13.0, 12.0, -14.0])
+    elif which == "permuted rows":
+        cell = base[[2, 0, 1]]
+    else:
+        cell = np.array([[3.0, 0.0, 0.0], [2.6, 1.5, 0.0], [1.0, 1.2, 2.8]])
+        r = 9.0
+    pos, _ = _rand(200 if which != "tiny skewed" else 20, 1.0, 91, dtype=np.float64, lo=-1.2, hi=2.2, cell=cell)
+    for pbc in [(1, 1, 1), (1, 0, 1)]:
+        check_parity(pos, cell, pbc, r, cuda, name=f"{which} pbc={pbc}")
+
+
+def test_errors_are_raised(cuda):
+    """Non-finite positions and explicit targets outside [0, N) raise RuntimeError (the
+    reference has no check; here the build reports them instead of producing garbage)."""
+    p, c = _rand(500, 20.0, 92)
+    pt = torch.from_numpy(p).to(cuda)
+    bad = pt.clone()
+    bad[17, 1] = float("nan")
+    with pytest.raises(RuntimeError, match="non-finite"):
+        impl.radius_graph_pbc(bad, torch.from_numpy(c), torch.tensor([True] * 3), 5.0, 0, False)
+    for t in (500, -1):
+        tg = torch.tensor([0, 3, t], dtype=torch.int64, device=cuda)
+        with pytest.raises(RuntimeError, match="target"):
+            impl.radius_graph_pbc_ex(pt, torch.from_numpy(c), torch.tensor([True] * 3), 5.0, 0, False, tg)
+    # and a good build right after still works
+    check_parity(p, c, (1, 1, 1), 5.0, cuda, name="after errors")
