@@ -43,10 +43,12 @@ def main():
                          "HBM before the timed region); 0 = the same positions every step.  "
                          "Default: 100 for C5 (its stated 100 rebuilds at 0.01 A per step), else 0")
     ap.add_argument("--sigma", type=float, default=0.01)
-    ap.add_argument("--path", default="graph", choices=["graph", "halo", "filter"],
+    ap.add_argument("--path", default="graph", choices=["graph", "halo", "filter", "batch"],
                     help="graph: the headline full rebuild; halo: extract_halo_info of one rank "
                          "of an 8-way SFC partition of the same box (edges at r + 0.5); filter: "
-                         "filter_edges_to_radius of the box's edges at r + 0.5 down to r")
+                         "filter_edges_to_radius of the box's edges at r + 0.5 down to r; batch: "
+                         "radius_graph_pbc_cuda on batches of small structures, batched against "
+                         "the per-structure loop")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -77,6 +79,8 @@ def main():
         return bench_halo(args)
     if args.path == "filter":
         return bench_filter(args)
+    if args.path == "batch":
+        return bench_batch(args)
 
     box = {"C1": configs.fcc, "C2": configs.c2, "C3": configs.c3, "C4": configs.c4,
            "C4-500k": lambda: configs.c4(scale=1.3934), "C5": configs.c5}[args.config]()
@@ -377,6 +381,59 @@ def bench_filter(args):
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "dg_filter_compact (single pass, all kernels)",
                      "algorithmic_bytes": nbytes}}), flush=True)
+
+
+def bench_batch(args):
+    """radius_graph_pbc_cuda on batches of small periodic structures (uniform at 0.08
+    atoms/A^3, r = 6 A, fp32): the batched build (one launch sequence per batch) against the
+    per-structure loop the reference runs.  One line per (structures, atoms per structure);
+    one step = one wrapper call, the host clock around `--steps` calls."""
+    import importlib
+    import types
+
+    import numpy as np
+    import torch
+
+    wrap = importlib.import_module("dynamis_amd.dynamis_state.radius_graph_pbc_cuda")
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    rng = np.random.default_rng(1)
+    for B in (8, 32, 128, 512):
+        for nat in (30, 100, 250, 500):
+            natoms = rng.integers(nat // 2, nat + 1, B)
+            cells, pos = [], []
+            for n in natoms:
+                L = (n / 0.08) ** (1 / 3)
+                cells.append(np.eye(3) * L)
+                pos.append(rng.uniform(0, L, (n, 3)))
+            data = types.SimpleNamespace(
+                pos=torch.from_numpy(np.concatenate(pos).astype(np.float32)).to(dev),
+                cell=torch.from_numpy(np.array(cells)).float().to(dev),
+                natoms=torch.from_numpy(natoms).to(dev), pbc=torch.tensor([[True] * 3] * B).to(dev))
+
+            def timed(max_atoms):
+                old = wrap.BATCH_MAX_ATOMS
+                wrap.BATCH_MAX_ATOMS = max_atoms
+                try:
+                    for _ in range(max(1, args.warmup)):
+                        wrap.radius_graph_pbc_cuda(data, 6.0, 0)
+                    torch.cuda.synchronize()
+                    t = time.perf_counter()
+                    for _ in range(args.steps):
+                        out = wrap.radius_graph_pbc_cuda(data, 6.0, 0)
+                    torch.cuda.synchronize()
+                    return (time.perf_counter() - t) * 1e3 / args.steps, out
+                finally:
+                    wrap.BATCH_MAX_ATOMS = old
+
+            chosen = wrap._batch_in_one_pass([int(x) for x in natoms])
+            ms_batch, out = timed(10 ** 9)  # (the batched build, whatever the cost model says)
+            ms_loop, _ = timed(0)
+            print(json.dumps({"metric": "radius_graph_pbc_cuda ms per batch", "structures": B,
+                              "atoms_per_structure_max": nat, "atoms": int(natoms.sum()),
+                              "edges": int(out[0].shape[1]), "batched_ms": round(ms_batch, 4),
+                              "loop_ms": round(ms_loop, 4), "speedup": round(ms_loop / ms_batch, 2),
+                              "batched_chosen": chosen, "steps": args.steps}), flush=True)
 
 
 def bench_halo(args):

@@ -49,6 +49,19 @@ class HaloDesc(ctypes.Structure):
     ]
 
 
+class BatchDesc(ctypes.Structure):
+    """dg_batch_desc."""
+
+    _fields_ = [
+        ("n_images", ctypes.c_int64),
+        ("n_atoms", ctypes.c_int64),
+        ("pos_dtype", ctypes.c_int32),
+        ("pbc", ctypes.c_uint8 * 3),
+        ("pad_", ctypes.c_uint8),
+        ("radius", ctypes.c_double),
+    ]
+
+
 _lib = None
 
 _p = ctypes.c_void_p
@@ -93,6 +106,10 @@ def lib():
         "dg_halo_count": (_i32, [ctypes.POINTER(HaloDesc), _p, _p, _p, _p, _p, _p, _p, _p, _sz, _p]),
         "dg_halo_read_totals": (_i32, [_p, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _p]),
         "dg_halo_write": (_i32, [ctypes.POINTER(HaloDesc), _p, _p, _p, _p, _p, _sz, _p]),
+        "dg_batch_workspace_size": (_sz, [ctypes.POINTER(BatchDesc)]),
+        "dg_batch_count": (_i32, [ctypes.POINTER(BatchDesc), _p, _p, _p, _p, _p, _sz, _p]),
+        "dg_batch_read_totals": (_i32, [ctypes.POINTER(BatchDesc), _p, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _p]),
+        "dg_batch_write": (_i32, [ctypes.POINTER(BatchDesc), _p, _p, _sz, _i64, _p, _p, _p, _p, _p]),
         "dg_last_error": (ctypes.c_char_p, []),
         "dg_version": (ctypes.c_char_p, []),
     }

@@ -15,7 +15,7 @@ HERE = os.path.dirname(os.path.abspath(__file__))
 ROOT = os.path.dirname(HERE)
 CSRC = os.path.join(HERE, "csrc")
 LIB = os.path.join(HERE, "libdynamis_graph.so")
-SOURCES = ["dg_graph.hip", "dg_count.hip", "dg_sfc.hip", "dg_halo.hip"]
+SOURCES = ["dg_graph.hip", "dg_count.hip", "dg_sfc.hip", "dg_halo.hip", "dg_batch.hip"]
 # Per-source flags.  The count kernel's sweep is bound by VALU issue: LLVM's iterative ILP
 # scheduler orders it better (C3 count 0.464 -> 0.440 ms), while the default scheduler
 # suits the store-bound write kernels of dg_graph.hip (0.660 vs 0.671 ms under ILP).

@@ -1661,7 +1661,8 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
 struct BruteArgs {
     double C[9], Cinv[9];
     double r2;
-    int pbc[3], kimg[3];
+    double cf[3];  // r / face distance per axis: the fractional reach of the cutoff sphere
+    int pbc[3];
     const void* pos;
     int f64;
     int64_t n, nt;
@@ -1679,12 +1680,6 @@ struct BruteArgs {
     int64_t* totals;
 };
 
-__device__ __forceinline__ void brute_floor(const BruteArgs& a, const double* p, int* f)
-{
-#pragma unroll
-    for (int j = 0; j < 3; ++j) f[j] = (int)floor(canon_frac(p[0], p[1], p[2], a.Cinv, j));
-}
-
 template <bool WRITE>
 __global__ void brute_kernel(BruteArgs a)
 {
@@ -1696,10 +1691,9 @@ __global__ void brute_kernel(BruteArgs a)
         if (!WRITE) { a.cnt[t] = 0; if (a.counts_user) a.counts_user[t] = 0; }
         return;
     }
-    double pt[3];
-    int ft[3];
+    double pt[3], frt[3];
     load_pos(a.pos, a.f64, tg, pt);
-    brute_floor(a, pt, ft);
+    for (int d = 0; d < 3; ++d) frt[d] = canon_frac(pt[0], pt[1], pt[2], a.Cinv, d);
     int64_t o = WRITE ? a.offs[t] : 0;
     if (WRITE && a.offs[t + 1] > a.capacity) {
         atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
@@ -1708,16 +1702,21 @@ __global__ void brute_kernel(BruteArgs a)
     int found = 0;
     for (int64_t j = 0; j < a.n; ++j) {
         double ps[3];
-        int fs[3];
         load_pos(a.pos, a.f64, j, ps);
-        brute_floor(a, ps, fs);
         // an edge's shift is its periodic image plus the floor difference of the two atoms
-        // (radius_graph_kernels.cu:282-303): images |I_d| <= kimg_d around ft - fs
+        // (radius_graph_kernels.cu:282-303); on a periodic axis every S with
+        // |frt - frs - S| <= cf can be one (the source image is at least that fractional
+        // distance times the face distance from the target), widened by 1e-9 against
+        // rounding; without PBC only the floor difference
         int lo[3], hi[3];
         for (int d = 0; d < 3; ++d) {
-            const int df = ft[d] - fs[d];
-            if (a.pbc[d]) { lo[d] = df - a.kimg[d]; hi[d] = df + a.kimg[d]; }
-            else { lo[d] = hi[d] = df; }
+            const double frs = canon_frac(ps[0], ps[1], ps[2], a.Cinv, d);
+            if (a.pbc[d]) {
+                lo[d] = (int)ceil(frt[d] - frs - a.cf[d] - 1e-9);
+                hi[d] = (int)floor(frt[d] - frs + a.cf[d] + 1e-9);
+            } else {
+                lo[d] = hi[d] = (int)floor(frt[d]) - (int)floor(frs);
+            }
         }
         for (int s0 = lo[0]; s0 <= hi[0]; ++s0)
             for (int s1 = lo[1]; s1 <= hi[1]; ++s1)
@@ -1943,7 +1942,7 @@ BruteArgs brute_args(const Plan& p, const void* pos, const int64_t* tgt, void* w
     memcpy(b.C, p.C, sizeof b.C);
     memcpy(b.Cinv, p.Cinv, sizeof b.Cinv);
     b.r2 = p.r2;
-    for (int d = 0; d < 3; ++d) { b.pbc[d] = p.pbc[d]; b.kimg[d] = p.kimg[d]; }
+    for (int d = 0; d < 3; ++d) { b.pbc[d] = p.pbc[d]; b.cf[d] = p.cf[d]; }
     b.pos = pos;
     b.f64 = p.f64;
     b.n = p.n;

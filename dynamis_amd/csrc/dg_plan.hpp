@@ -43,7 +43,6 @@ struct Plan {
     int64_t ntiles = 0, nbins = 0, ncodes = 0;
     int nregion = 0;
     int brute = 0;          // region too large: all-pairs path
-    int kimg[3];            // brute path: |S_d| range on periodic axes
     float hi = 0, lo_in = 0, tiny = 0;
     float toff = 0, hi_off = 0;  // the same bounds on d2 - toff (see plan_grid)
     uint32_t lo_bits = 0;        // bits of the fp32 bound lo_off on d2 - toff
@@ -162,7 +161,6 @@ inline void plan_grid(Plan& p)
         int b = 0;
         while ((1 << b) < p.ntl[d]) b++;
         p.mb[d] = b;
-        p.kimg[d] = p.pbc[d] ? (int)ceil(p.cf[d]) + 1 : 0;
     }
     p.nregion = p.R[0] * p.R[1] * p.R[2];
     p.tb = p.T[0] * p.T[1] * p.T[2];

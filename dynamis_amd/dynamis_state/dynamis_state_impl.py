@@ -143,6 +143,55 @@ def build_graph(pos, cell, pbc, radius, target_indices=None, counts_only=False,
         return out
 
 
+def build_batch(pos, cells, natoms, pbc, radius, max_num_neighbors=0):
+    """Graphs of a batch of structures in one launch sequence (dg_batch_*): the batched
+    form of radius_graph_pbc_cuda's per-structure loop (radius_graph_pbc_cuda.py:64-110).
+
+    pos [N, 3] (the structures one after another), cells [B, 3, 3], natoms [B], pbc [3]
+    shared by the batch.  Returns (edge_index [2, E] with batch atom indices, cell_offsets
+    [E, 3] float32, num_neighbors_image [B] int64).  Edges are grouped by target,
+    structures in batch order, targets in index order.
+    """
+    pos, _, pbc, _ = _validate(pos, torch.eye(3), pbc, radius, max_num_neighbors)
+    lib = L.lib()
+    dev = pos.device
+    B = int(natoms.numel())
+    _check(B >= 1, "the batch is empty")
+    cells = torch.as_tensor(cells)
+    _check(cells.dim() == 3 and cells.size(0) == B and cells.size(1) == 3 and cells.size(2) == 3,
+           f"cell must have shape [{B}, 3, 3], got {_shape(cells)}")
+    d = L.BatchDesc()
+    d.n_images = B
+    d.n_atoms = pos.size(0)
+    d.pos_dtype = L.DG_F64 if pos.dtype == torch.float64 else L.DG_F32
+    for k in range(3):
+        d.pbc[k] = 1 if bool(pbc[k]) else 0
+    d.radius = _r32(radius)
+    # the cell rounded to the position dtype, as the single-structure binding does
+    # (radius_graph.cpp:24)
+    c = cells.to(device=dev, dtype=pos.dtype).to(torch.float64).contiguous()
+    na = torch.as_tensor(natoms).to(device=dev, dtype=torch.int64).contiguous()
+    wsb = lib.dg_batch_workspace_size(d)
+    if wsb == 0:
+        raise RuntimeError(lib.dg_last_error().decode())
+    with torch.cuda.device(dev):
+        s = L.stream_of(dev)
+        ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+        L.check(lib.dg_batch_count(d, L.ptr(pos), L.ptr(na), L.ptr(c), None, L.ptr(ws), wsb, s),
+                "radius_graph_pbc_cuda")
+        E, fl = L._i64(0), L._i64(0)
+        L.check(lib.dg_batch_read_totals(d, L.ptr(ws), E, fl, s), "radius_graph_pbc_cuda")
+        E = int(E.value)
+        edge_index = torch.empty((2, E), dtype=torch.long, device=dev)
+        shifts = torch.empty((E, 3), dtype=torch.float32, device=dev)
+        nn = torch.empty(B, dtype=torch.long, device=dev)
+        base = edge_index.data_ptr()
+        L.check(lib.dg_batch_write(d, L.ptr(pos), L.ptr(ws), wsb, E, L.ctypes.c_void_p(base),
+                                   L.ctypes.c_void_p(base + 8 * E), L.ptr(shifts), L.ptr(nn), s),
+                "radius_graph_pbc_cuda")
+    return edge_index, shifts, nn
+
+
 def _r32(radius) -> float:
     # the reference binds radius as C++ float (radius_graph.cpp:7)
     return float(np.float32(radius))

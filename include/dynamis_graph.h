@@ -221,6 +221,47 @@ dg_status dg_sfc_labels(const int64_t* perm, int64_t n, int64_t n_parts, const i
  * Two stages on one workspace of dg_halo_workspace_size(n_atoms, world_size) bytes:
  * dg_halo_count (offsets + interior mask), dg_halo_read_totals (synchronous), then
  * dg_halo_write (the index lists, into buffers of the read sizes). */
+/* ------------------------------------------------------------------ batches of structures
+ * radius_graph_pbc_cuda with a batch (radius_graph_pbc_cuda.py:64-110) builds structure by
+ * structure.  These entry points build the graphs of a whole batch of small structures
+ * (all sharing the PBC flags and radius, each with its own cell) in one launch sequence:
+ * all-pairs over each structure's atoms and periodic images, the canonical fp64 predicate
+ * and shift convention of dg_graph_*.  Edges come grouped by target: structures in batch
+ * order, targets in index order (within a target the order is fixed but unspecified).
+ * The atom indices are those of the batch (structure b's atoms follow structures 0..b-1). */
+typedef struct dg_batch_desc {
+    int64_t n_images;   /* structures in the batch (>= 1) */
+    int64_t n_atoms;    /* atoms of the whole batch */
+    int32_t pos_dtype;  /* DG_F32 / DG_F64 */
+    uint8_t pbc[3];     /* shared by every structure */
+    double radius;      /* cutoff (rounded to fp32 by the caller, as dg_graph_desc) */
+} dg_batch_desc;
+
+size_t dg_batch_workspace_size(const dg_batch_desc* desc);
+
+/* Stage 1: per-atom degrees and the batch's edge count.
+ *   pos      device [n_atoms,3] of pos_dtype, the structures one after another
+ *   natoms   device int64 [n_images], atoms per structure (summing to n_atoms)
+ *   cells    device float64 [n_images,3,3], row-major lattice vectors (rounded to
+ *            pos_dtype by the caller, as dg_graph_desc.cell)
+ *   counts_out  device int32 [n_atoms] or NULL
+ * Asynchronous; then dg_batch_read_totals. */
+dg_status dg_batch_count(const dg_batch_desc* desc, const void* pos, const int64_t* natoms,
+                         const double* cells, int32_t* counts_out, void* workspace,
+                         size_t workspace_bytes, hipStream_t stream);
+
+/* Synchronous: the batch's edge count and status flags.  DG_ERR_INVALID for a singular
+ * cell or atom counts that do not add up, DG_ERR_RANGE for non-finite positions. */
+dg_status dg_batch_read_totals(const dg_batch_desc* desc, const void* workspace,
+                               int64_t* total_edges, int64_t* flags, hipStream_t stream);
+
+/* Stage 2: every edge, into outputs of `capacity` rows, and the edge count of every
+ * structure (edges_per_image: device int64 [n_images] or NULL; "num_neighbors_image"). */
+dg_status dg_batch_write(const dg_batch_desc* desc, const void* pos, void* workspace,
+                         size_t workspace_bytes, int64_t capacity, int64_t* edge_src,
+                         int64_t* edge_dst, float* cell_shift, int64_t* edges_per_image,
+                         hipStream_t stream);
+
 typedef struct dg_halo_desc {
     int64_t n_atoms;    /* N: length of pid, range of atom ids */
     int64_t n_edges;    /* E */
