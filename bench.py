@@ -26,6 +26,7 @@ sys.path.insert(0, ROOT)
 
 HBM_PEAK_GBS = 8000.0
 WRITE_BYTES_PER_EDGE = 28   # edge_index int64 x2 + cell shift fp32 x3
+VECTOR_BYTES_PER_EDGE = 16  # with --vectors: edge vector fp32 x3 + distance fp32
 METRIC = "Gedges/s and ms per full rebuild, 1M atoms r_cut=6 Å, 1 GPU; % HBM peak"
 
 
@@ -43,6 +44,9 @@ def main():
                          "HBM before the timed region); 0 = the same positions every step.  "
                          "Default: 100 for C5 (its stated 100 rebuilds at 0.01 A per step), else 0")
     ap.add_argument("--sigma", type=float, default=0.01)
+    ap.add_argument("--vectors", action="store_true",
+                    help="graph path: also emit the edge vectors (fp32 [E,3]) and distances "
+                         "(fp32 [E]) in the write stage: 44 bytes per edge instead of 28")
     ap.add_argument("--path", default="graph", choices=["graph", "halo", "filter", "batch"],
                     help="graph: the headline full rebuild; halo: extract_halo_info of one rank "
                          "of an 8-way SFC partition of the same box (edges at r + 0.5); filter: "
@@ -114,6 +118,11 @@ def main():
     src = torch.empty(cap, dtype=torch.int64, device=dev)
     dst = torch.empty(cap, dtype=torch.int64, device=dev)
     shift = torch.empty((cap, 3), dtype=torch.float32, device=dev)
+    vec = dist = None
+    if args.vectors:
+        vec = torch.empty((cap, 3), dtype=torch.float32, device=dev)
+        dist = torch.empty(cap, dtype=torch.float32, device=dev)
+    bpe = WRITE_BYTES_PER_EDGE + (VECTOR_BYTES_PER_EDGE if args.vectors else 0)
 
     # position frames: a random walk of sigma per coordinate per frame (seeded), generated
     # on the device before any timing
@@ -131,7 +140,7 @@ def main():
         if ev is not None:
             ev[0].record(stream)
         L.check(lib.dg_graph_write(d, L.ptr(p), L.ptr(tgt), L.ptr(ws), wsb, cap, L.ptr(src), L.ptr(dst),
-                                   L.ptr(shift), None, None, 0, s), "write")
+                                   L.ptr(shift), L.ptr(vec), L.ptr(dist), 0, s), "write")
         if ev is not None:
             ev[1].record(stream)
 
@@ -168,31 +177,38 @@ def main():
 
     cell_t = torch.from_numpy(np.asarray(box.cell))
     pbc_t = torch.tensor(list(box.pbc))
+    def api_call():
+        if args.vectors:
+            impl.radius_graph_pbc_vectors(pos, cell_t, pbc_t, box.radius, tgt, torch.float32)
+        else:
+            impl.radius_graph_pbc_ex(pos, cell_t, pbc_t, box.radius, 0, False, tgt)
+
     for _ in range(2):
-        impl.radius_graph_pbc_ex(pos, cell_t, pbc_t, box.radius, 0, False, tgt)
+        api_call()
     torch.cuda.synchronize()
     ta = time.perf_counter()
     api_steps = max(3, args.steps // 4)
     for _ in range(api_steps):
-        impl.radius_graph_pbc_ex(pos, cell_t, pbc_t, box.radius, 0, False, tgt)
+        api_call()
     torch.cuda.synchronize()
     api_ms = (time.perf_counter() - ta) * 1e3 / api_steps
 
     pos_bytes = 24 if pos.dtype == torch.float64 else 12
     # Full-rebuild algorithmic bytes: read positions, keys write+read, reordered positions
     # write+read, the edge outputs (28 B per edge: int64 src, int64 dst, 3 x fp32 shift).
-    rebuild_bytes = pos_bytes * n + 16 * n + 24 * n + WRITE_BYTES_PER_EDGE * E
+    rebuild_bytes = pos_bytes * n + 16 * n + 24 * n + bpe * E
     # Dominant kernel (the write stage), algorithmic bytes per launch: the edge outputs
     # only.  Everything else it moves (the count pass's slot entries, the cell list, the
     # tile tables) is an intermediate of this design and shows up in `traffic`.
-    kbytes = WRITE_BYTES_PER_EDGE * E
+    kbytes = bpe * E
     achieved = kbytes / (write_ms * 1e-3) / 1e9
 
     # HBM bytes per launch of the write stage measured by rocprofv3 (FETCH_SIZE +
     # WRITE_SIZE, scaled by a plain copy of known size); recorded in profiles/ by the
     # commands written there, for this config.
     traffic = None
-    tfile = os.path.join(ROOT, "profiles", f"edge_write_{args.config}_traffic.json")
+    tfile = os.path.join(ROOT, "profiles", f"edge_write_{args.config}{'_vectors' if args.vectors else ''}"
+                                           "_traffic.json")
     if os.path.exists(tfile):
         try:
             traffic = json.load(open(tfile)).get("bytes_per_launch")
@@ -232,12 +248,14 @@ def main():
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_over_algorithmic": round(traffic / kbytes, 3) if traffic else None,
                      "kernel": "expand_kernel (+ search_kernel<1> fix-up): the write stage",
-                     "algorithmic_bytes": kbytes, "bytes_per_unit": "28 per edge",
+                     "algorithmic_bytes": kbytes, "bytes_per_unit": f"{bpe} per edge",
                      "launch_ms": round(write_ms, 4)},
         "cpu_baseline": cpu,
     }
     if pos.dtype == torch.float64:
         out["dtype"] = "fp64 positions, fp64 predicate, int64 edges"
+    if args.vectors:
+        out["config"]["outputs"] = "edge_index, cell shifts, fp32 edge vectors and distances"
     print(json.dumps(out), flush=True)
 
 

@@ -612,6 +612,7 @@ struct SearchArgs {
     const float4* spos;
     const uint32_t* sflr;
     const int* sid;    // atom id of every cell-list entry
+    const void* cpos;  // the positions in cell-list order (pos dtype; set for vector outputs)
     const int* bstart;
     const int* tile_of_rank;
     const int* rank_of_tile;
@@ -687,12 +688,13 @@ __device__ __forceinline__ int64_t xcd_tile_rank(int64_t b, int64_t ntiles)
 // CU; the fix-up write pass adds the per-entry shift table T.
 constexpr int kStage = 64 * kExpandIlp;  // edges one wave stages per step
 // CAP: region entries staged (one LDS chunk, or two for the dense tiles of expand2)
-template <int CAP>
+// STG: edges a wave stages per step (64 per unit of the expansion's ILP)
+template <int CAP, int STG = kStage>
 struct ExpandStageT {
     int2 e[CAP + 1];  // per region entry: source atom id, packed (bin shift - floor)
-    int st_src[kBlock / 64][kStage];
-    int st_dst[kBlock / 64][kStage];
-    uint32_t st_S[kBlock / 64][kStage];
+    int st_src[kBlock / 64][STG];
+    int st_dst[kBlock / 64][STG];
+    uint32_t st_S[kBlock / 64][STG];
 };
 typedef ExpandStageT<kCap> ExpandStage;
 struct BatchTab {
@@ -743,6 +745,21 @@ struct Expand2Lds {
 };
 template <int CAP> struct ExpandLdsOf { typedef ExpandLds type; };
 template <> struct ExpandLdsOf<2 * kCap> { typedef Expand2Lds type; };
+// Per wave, the edge vectors and distances of one step (STG edges) as the bytes they take
+// in the outputs (v: 3 per edge, d: 1 per edge), so 16-byte chunks go out as they are.
+template <typename VT, int STG>
+struct VecStageT {
+    __align__(16) VT v[kBlock / 64][3 * STG];
+    __align__(16) VT d[kBlock / 64][STG];
+};
+// The expansion with edge vectors / distances of type VT, in steps of 64 * kVecIlp edges.
+// (Half the steps -- 8 KB less staging, four workgroups per CU for fp32 vectors -- measured
+// slower: C3 1.27 vs 1.21 ms.)
+constexpr int kVecIlp = kExpandIlp;
+template <typename VT>
+struct ExpandVLds : ExpandLds {
+    VecStageT<VT, 64 * kVecIlp> vs;
+};
 static_assert(sizeof(CountLds) <= 40960, "count pass must fit four workgroups per CU");
 template <int MODE>
 struct LdsOf { typedef CountLds type; };
@@ -872,7 +889,8 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // Stages the tile's region into ExpandStage::e as (source atom id, packed bin shift -
 // floor) pairs -- 8 bytes per entry -- bin by bin from the cell list.  The caller has
 // finished every use of the float4 view of the region buffer.
-template <int CAP>
+// GIDX: an entry names its source by cell-list index instead of atom id.
+template <int CAP, bool GIDX = false>
 __device__ __forceinline__ void stage_pairs(const SearchArgs& a, typename ExpandLdsOf<CAP>::type& sh,
                                             const int* g0)
 {
@@ -897,7 +915,7 @@ __device__ __forceinline__ void stage_pairs(const SearchArgs& a, typename Expand
                 for (int i = 0; i < rcnt[h]; ++i) {
                     const int gidx = rst[h] + i;
                     const uint32_t fl = a.sflr[gidx];
-                    X.e[ex + i] = make_int2(a.sid[gidx], (int)pack3(sb[0] - unpack3(fl, 0),
+                    X.e[ex + i] = make_int2(GIDX ? gidx : a.sid[gidx], (int)pack3(sb[0] - unpack3(fl, 0),
                                                                      sb[1] - unpack3(fl, 1),
                                                                      sb[2] - unpack3(fl, 2)));
                 }
@@ -913,17 +931,25 @@ __device__ __forceinline__ void stage_pairs(const SearchArgs& a, typename Expand
 // stage_pairs; ebase = output offset of the tile's first edge).  Each batch of up to 256
 // targets has its edges split evenly over the waves; a wave walks its range 64 edges at a
 // time, lane e finding its target by a short forward walk from the wave's current target.
-// Edges k >= K are left to search_kernel<1>.  PLAIN: no vector / distance outputs.
-template <bool PLAIN, int CAP>
+// Edges k >= K are left to search_kernel<1>.
+// PLAIN: edges go out in 16-byte groups staged in LDS; with VT (float or double) the edge
+// vectors and distances too, staged in *vsp (a VecStageT<VT>); without PLAIN every edge is
+// written by its lane (emit_edge, vectors included).
+template <bool PLAIN, int CAP, typename VT = void, int ILP = kExpandIlp>
 __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename ExpandLdsOf<CAP>::type& sh,
-                                            int tbeg, int ntg, int64_t ebase)
+                                            int tbeg, int ntg, int64_t ebase, void* vsp = nullptr)
 {
-    ExpandStageT<CAP>& X = *(ExpandStageT<CAP>*)sh.qbuf;
+    static_assert(ILP % 2 == 0, "two edges per 16-byte chunk of sources / targets");
+    constexpr int kStg = 64 * ILP;  // edges a wave stages per step
+    ExpandStageT<CAP, kStg>& X = *(ExpandStageT<CAP, kStg>*)sh.qbuf;
     BatchTab& B = sh.bt;
     const int lane = threadIdx.x & 63;
     const int w = threadIdx.x >> 6;
     const int NWv = kBlock / 64;
     constexpr bool plain = PLAIN;
+    constexpr bool kVec = !std::is_void<VT>::value;
+    static_assert(PLAIN || !kVec, "the per-lane path writes vectors itself");
+    typedef typename std::conditional<kVec, VT, float>::type VTn;  // (a type when VT is void)
     for (int k0 = 0; k0 < ntg; k0 += kBlock) {
         const int nbatch = min(kBlock, ntg - k0);
         const int j = tbeg + k0 + threadIdx.x;
@@ -954,23 +980,23 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
         const char* __restrict__ sl = (const char*)a.slot + (size_t)16 * (tbeg + k0);
         const uint64_t gstep = 16ull * (uint64_t)a.nslot;  // bytes between a target's groups
 
-        // Edges [b0, b1) of the batch (b1 - b0 <= 64 * kExpandIlp), lane-strided: edge
+        // Edges [b0, b1) of the batch (b1 - b0 <= 64 * ILP), lane-strided: edge
         // b0 + 64u + lane -> source id, target id, packed shift; ok = false past b1 or for
         // k >= K (left to search_kernel<1>).  All slot loads are issued before the first
         // entry is looked up.  Advances tcur to the target of edge b1 - 1.
         // Two halves: locate() finds (target, k) of edges [b0, b1) and issues their slot
         // loads -- unconditionally (edges past b1 or with k >= K load a valid dummy), so all
-        // kExpandIlp loads are in flight together -- and advances tcur to the target of
+        // ILP loads are in flight together -- and advances tcur to the target of
         // edge b1 - 1; resolve() turns them into (source id, target id, packed shift).  The
         // plain path locates the next step before storing this one, so the wait on its
         // loads does not also wait on the stores (the memory counter is shared).
         struct Loc {
-            int tt[kExpandIlp], kk[kExpandIlp], raw[kExpandIlp];
+            int tt[ILP], kk[ILP], raw[ILP];
         };
         auto locate = [&](int b0, int b1, Loc& L) {
             int t = tcur;
 #pragma unroll
-            for (int u = 0; u < kExpandIlp; ++u) {
+            for (int u = 0; u < ILP; ++u) {
                 const int e = b0 + 64 * u + lane;
                 L.kk[u] = a.K;
                 L.tt[u] = t;
@@ -981,7 +1007,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
                 }
             }
 #pragma unroll
-            for (int u = 0; u < kExpandIlp; ++u) {
+            for (int u = 0; u < ILP; ++u) {
                 const uint64_t at = L.kk[u] < a.K ? (uint64_t)(uint32_t)(L.kk[u] >> 3) * gstep +
                                                         (16u * (uint32_t)L.tt[u] + 2u * (L.kk[u] & 7))
                                                   : 0ull;
@@ -990,13 +1016,21 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
             // the lane holding edge b1 - 1 has its target in t
             if (b1 > b0) tcur = __builtin_amdgcn_readlane(t, (b1 - 1 - b0) & 63);
         };
+        // with vectors, region entries name their source by cell-list index (rg), which
+        // also indexes the positions in cell-list order
+        int rg[ILP];
         auto resolve = [&](const Loc& L, int* rs, int* rd, uint32_t* rS, bool* rok) {
 #pragma unroll
-            for (int u = 0; u < kExpandIlp; ++u) {
+            for (int u = 0; u < ILP; ++u) {
                 rok[u] = L.kk[u] < a.K;
                 const int2 en = X.e[rok[u] ? min(L.raw[u] >> 4, CAP) : CAP];
                 const uint32_t ft = B.tf[L.tt[u]];
-                rs[u] = en.x;
+                if constexpr (kVec) {
+                    rg[u] = en.x;
+                    rs[u] = a.sid[en.x];
+                } else {
+                    rs[u] = en.x;
+                }
                 rd[u] = B.tid[L.tt[u]];
                 rS[u] = pack3(unpack3((uint32_t)en.y, 0) + unpack3(ft, 0),
                               unpack3((uint32_t)en.y, 1) + unpack3(ft, 1),
@@ -1013,11 +1047,11 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
         auto store_lanes = [&](int b0, const int* rs, const int* rd, const uint32_t* rS,
                                const bool* rok) {
 #pragma unroll
-            for (int u = 0; u < kExpandIlp; ++u) {
+            for (int u = 0; u < ILP; ++u) {
                 if (!rok[u]) continue;
                 const int64_t o = wbase + (b0 + 64 * u + lane - E0);
                 const int S0 = unpack3(rS[u], 0), S1 = unpack3(rS[u], 1), S2 = unpack3(rS[u], 2);
-                if constexpr (plain) {
+                if constexpr (plain && !kVec) {
                     __builtin_nontemporal_store((int64_t)rs[u], a.out_src + o);
                     __builtin_nontemporal_store((int64_t)rd[u], a.out_dst + o);
                     const v3f sv = {(float)S0, (float)S1, (float)S2};
@@ -1028,12 +1062,12 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
             }
         };
 
-        int rs[kExpandIlp], rd[kExpandIlp];
-        uint32_t rS[kExpandIlp];
-        bool rok[kExpandIlp];
+        int rs[ILP], rd[ILP];
+        uint32_t rS[ILP];
+        bool rok[ILP];
         if constexpr (!plain) {
-            for (int b0 = E0; b0 < E1; b0 += 64 * kExpandIlp) {
-                fetch(b0, min(E1, b0 + 64 * kExpandIlp), rs, rd, rS, rok);
+            for (int b0 = E0; b0 < E1; b0 += 64 * ILP) {
+                fetch(b0, min(E1, b0 + 64 * ILP), rs, rd, rS, rok);
                 store_lanes(b0, rs, rd, rS, rok);
             }
         } else {
@@ -1053,18 +1087,52 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
             int* st_s = X.st_src[w];
             int* st_d = X.st_dst[w];
             uint32_t* st_S = X.st_S[w];
-            // Full steps of 64 * kExpandIlp edges run branch-free: the next step's slot loads
+            // with vectors: this lane's edges' canonical vectors and distances (fp64, as
+            // emit_edge computes them), and the wave's staging rows for them
+            VTn rv[ILP][3], rdd[ILP];
+            VTn* st_v = nullptr;
+            VTn* st_dd = nullptr;
+            if constexpr (kVec) {
+                VecStageT<VTn, kStg>& VS = *(VecStageT<VTn, kStg>*)vsp;
+                st_v = VS.v[w];
+                st_dd = VS.d[w];
+            }
+            auto vectors = [&]() {
+                if constexpr (kVec) {
+#pragma unroll
+                    for (int u = 0; u < ILP; ++u) {
+                        double ps[3], pt[3], vv[3];
+                        load_pos(a.cpos, a.f64, rg[u], ps);  // (cell-list order: local)
+                        load_pos(a.pos, a.f64, rd[u], pt);
+                        const double dd = canon_d2(ps, pt, unpack3(rS[u], 0), unpack3(rS[u], 1),
+                                                   unpack3(rS[u], 2), a.C, vv);
+                        rv[u][0] = (VTn)vv[0];
+                        rv[u][1] = (VTn)vv[1];
+                        rv[u][2] = (VTn)vv[2];
+                        rdd[u] = (VTn)sqrt(dd);
+                    }
+                }
+            };
+            // Full steps of 64 * ILP edges run branch-free: the next step's slot loads
             // are issued before this step's stores and consumed right behind them, in
             // straight-line code, so the wait on the loads leaves the stores in flight (the
             // memory counter is shared by loads and stores).  The last, partial step is
             // masked.
-            constexpr int kStep = 64 * kExpandIlp;
+            constexpr int kStep = 64 * ILP;
             const int nfull = (A1 - A0) / kStep;
             auto stage = [&](int n) {
 #pragma unroll
-                for (int u = 0; u < kExpandIlp; ++u) {
+                for (int u = 0; u < ILP; ++u) {
                     const int i = 64 * u + lane;
-                    if (i < n) { st_s[i] = rs[u]; st_d[i] = rd[u]; st_S[i] = rS[u]; }
+                    if (i < n) {
+                        st_s[i] = rs[u]; st_d[i] = rd[u]; st_S[i] = rS[u];
+                        if constexpr (kVec) {
+                            st_v[3 * i] = rv[u][0];
+                            st_v[3 * i + 1] = rv[u][1];
+                            st_v[3 * i + 2] = rv[u][2];
+                            st_dd[i] = rdd[u];
+                        }
+                    }
                 }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
@@ -1076,10 +1144,13 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
                 v4i* __restrict__ os = (v4i*)(a.out_src + gb);
                 v4i* __restrict__ od = (v4i*)(a.out_dst + gb);
                 v4f* __restrict__ of = (v4f*)(a.out_shift + 3 * gb);
+                // chunks of a full step: kStg / 2 of sources (and of targets), 3 kStg / 4
+                // of shifts; a loop over them masks the chunks past its count
+                constexpr int kChE = kStg / 2, kChS = 3 * kStg / 4;
 #pragma unroll
-                for (int h = 0; h < kExpandIlp / 2; ++h) {
+                for (int h = 0; h < (kChE + 63) / 64; ++h) {
                     const int c = 64 * h + lane;  // 16-byte chunk: edges 2c, 2c + 1
-                    if (full || c < 2 * G) {
+                    if (c < (full ? kChE : 2 * G)) {
                         const v4i vs = {st_s[2 * c], 0, st_s[2 * c + 1], 0};
                         const v4i vd = {st_d[2 * c], 0, st_d[2 * c + 1], 0};
                         __builtin_nontemporal_store(vs, os + c);
@@ -1087,9 +1158,9 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
                     }
                 }
 #pragma unroll
-                for (int h = 0; h < 3 * kExpandIlp / 4; ++h) {
+                for (int h = 0; h < (kChS + 63) / 64; ++h) {
                     const int c = 64 * h + lane;  // 16-byte chunk: shift floats 4c .. 4c + 3
-                    if (full || c < 3 * G) {
+                    if (c < (full ? kChS : 3 * G)) {
                         float f[4];
 #pragma unroll
                         for (int i = 0; i < 4; ++i) {
@@ -1100,11 +1171,38 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
                         __builtin_nontemporal_store(vf, of + c);
                     }
                 }
+                if constexpr (kVec) {
+                    // the staged rows are the outputs' bytes: n edges are 3 n VT of vector
+                    // and n VT of distance, whole 16-byte chunks (n is a multiple of 4)
+                    constexpr int kPer = 16 / (int)sizeof(VTn);  // VT per chunk
+                    constexpr int kChV = 3 * kStg / kPer, kChD = kStg / kPer;
+                    if (a.out_vec) {
+                        v4i* __restrict__ ov = (v4i*)((VTn*)a.out_vec + 3 * gb);
+                        const v4i* sv = (const v4i*)st_v;
+#pragma unroll
+                        for (int h = 0; h < (kChV + 63) / 64; ++h) {
+                            const int c = 64 * h + lane;
+                            if (c < (full ? kChV : 3 * n / kPer)) __builtin_nontemporal_store(sv[c], ov + c);
+                        }
+                    }
+                    if (a.out_dist) {
+                        v4i* __restrict__ odd = (v4i*)((VTn*)a.out_dist + gb);
+                        const v4i* sd = (const v4i*)st_dd;
+#pragma unroll
+                        for (int h = 0; h < (kChD + 63) / 64; ++h) {
+                            const int c = 64 * h + lane;
+                            if (c < (full ? kChD : n / kPer)) __builtin_nontemporal_store(sd[c], odd + c);
+                        }
+                    }
+                }
                 __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
                 __builtin_amdgcn_wave_barrier();
                 __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
             };
-            if (A0 < A1) fetch(A0, min(A1, A0 + kStep), rs, rd, rS, rok);
+            if (A0 < A1) {
+                fetch(A0, min(A1, A0 + kStep), rs, rd, rS, rok);
+                vectors();
+            }
             for (int s0 = 0; s0 < nfull; ++s0) {
                 const int b0 = A0 + s0 * kStep;
                 stage(kStep);
@@ -1112,6 +1210,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
                 locate(b0 + kStep, min(A1, b0 + 2 * kStep), L);  // empty past A1: dummy loads
                 store_groups(wbase + (b0 - E0), kStep, std::true_type());
                 resolve(L, rs, rd, rS, rok);
+                vectors();
             }
             if (nfull * kStep < A1 - A0) {
                 const int b0 = A0 + nfull * kStep;
@@ -1584,9 +1683,11 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
 // Writes every edge the count pass left in the slots of tile ord (output order), from a
 // region staged for up to CAP entries: kCap for most tiles (expand_kernel), 2 kCap for the
 // two-chunk tiles (inside search_kernel<1>).
-template <int CAP>
+// VT: the type of the edge vectors / distances written in 16-byte groups from *vsp (void:
+// none, or written per lane).
+template <int CAP, typename VT = void>
 __device__ __forceinline__ void expand_one(const SearchArgs& a, typename ExpandLdsOf<CAP>::type& sh,
-                                           int64_t ord)
+                                           int64_t ord, void* vsp = nullptr)
 {
     const int64_t rank = xcd_tile_rank(ord, a.ntiles);
     const int* tstart = listed_targets(a) ? a.tbstart : a.bstart;
@@ -1603,8 +1704,10 @@ __device__ __forceinline__ void expand_one(const SearchArgs& a, typename ExpandL
     const int lin = a.tile_of_rank[rank];
     const int g0[3] = {(lin % a.ntl[0]) * a.T[0], ((lin / a.ntl[0]) % a.ntl[1]) * a.T[1],
                        (lin / (a.ntl[0] * a.ntl[1])) * a.T[2]};
-    stage_pairs<CAP>(a, sh, g0);
-    if (!a.out_vec && !a.out_dist)
+    stage_pairs<CAP, !std::is_void<VT>::value>(a, sh, g0);
+    if constexpr (!std::is_void<VT>::value)
+        expand_tile<true, CAP, VT, kVecIlp>(a, sh, tbeg, ntg, ebase, vsp);
+    else if (!a.out_vec && !a.out_dist)
         expand_tile<true, CAP>(a, sh, tbeg, ntg, ebase);
     else
         expand_tile<false, CAP>(a, sh, tbeg, ntg, ebase);
@@ -1646,12 +1749,39 @@ void launch_count_kernel(const SearchArgs& a, unsigned grid, hipStream_t s);
 // Writes every edge held in the count pass's slots, one workgroup per tile (the write
 // stage of the two-stage build; tiles whose region needs two LDS chunks are expanded by
 // search_kernel<1>, larger ones written by it directly).
+// The positions in cell-list order (entry g: atom sid[g]), for the edge vectors: the
+// expansion then reads a tile's sources from a few contiguous runs instead of from all
+// over the caller's order.
+__global__ void cell_pos_kernel(int64_t n, const int* __restrict__ sid, const void* __restrict__ pos,
+                                int f64, void* __restrict__ cpos)
+{
+    const int64_t g = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    if (g >= n) return;
+    const int64_t i = sid[g];
+    if (f64) {
+        const double* ps = (const double*)pos + 3 * i;
+        double* pc = (double*)cpos + 3 * g;
+        pc[0] = ps[0]; pc[1] = ps[1]; pc[2] = ps[2];
+    } else {
+        const float* ps = (const float*)pos + 3 * i;
+        float* pc = (float*)cpos + 3 * g;
+        pc[0] = ps[0]; pc[1] = ps[1]; pc[2] = ps[2];
+    }
+}
+
+// VT: void without vector / distance outputs, else their type.
+template <typename VT>
 __global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
 {
-    __shared__ ExpandLds sh;
     const int64_t ord = blockIdx.x;  // output order, as search_kernel
     if (a.tfix[ord] & (kFixChunked | kFix2)) return;
-    expand_one<kCap>(a, sh, ord);
+    if constexpr (std::is_void<VT>::value) {
+        __shared__ ExpandLds sh;
+        expand_one<kCap>(a, sh, ord);
+    } else {
+        __shared__ ExpandVLds<VT> sh;
+        expand_one<kCap, VT>(a, sh, ord, &sh.vs);
+    }
 }
 
 // ---------------------------------------------------------------- all-pairs fallback
@@ -1921,7 +2051,6 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.tfix = at<int>(ws, p.o_tfix);
     a.tbase = at<int64_t>(ws, p.o_tbase);
     a.totals = at<int64_t>(ws, p.o_tot);
-    // slots are addressed with 32-bit byte offsets; larger problems sweep twice instead
     // slot rows: one per target, or per atom when the targets are the atoms with ids < nt
     // (every atom of a tile is then a lane)
     const int64_t nrow = p.nrow;
@@ -2238,7 +2367,21 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
     a.capacity = capacity;
     StageTimer clk(s);
     clk.mark("start");
-    hipLaunchKernelGGL(expand_kernel, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    // vectors / distances go out in 16-byte groups from bases aligned to 16 bytes, else
+    // every edge is written by its lane
+    const bool vec = edge_vec || edge_dist;
+    const bool vec16 = vec && (((uintptr_t)edge_vec | (uintptr_t)edge_dist) & 15u) == 0;
+    if (vec16) {
+        a.cpos = at<char>(ws, p.o_cpos);
+        hipLaunchKernelGGL(cell_pos_kernel, dim3(nblocks(p.n, 256)), dim3(256), 0, s, (int64_t)p.n,
+                           (const int*)a.sid, pos, p.f64, (void*)a.cpos);
+    }
+    if (vec16 && a.vout_f64)
+        hipLaunchKernelGGL(expand_kernel<double>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    else if (vec16)
+        hipLaunchKernelGGL(expand_kernel<float>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
+    else
+        hipLaunchKernelGGL(expand_kernel<void>, dim3((unsigned)p.ntiles), dim3(kBlock), 0, s, a);
     clk.mark("write (slot expansion)");
     hipLaunchKernelGGL(search_kernel<1>, dim3((unsigned)std::min<int64_t>(p.ntiles, kFixGrid)), dim3(kBlock), 0, s, a);
     clk.mark("write (fix-up)");

@@ -48,6 +48,7 @@ struct Plan {
     uint32_t lo_bits = 0;        // bits of the fp32 bound lo_off on d2 - toff
     // workspace layout (byte offsets)
     size_t o_key, o_rank, o_rec, o_bcnt, o_bstart, o_sid, o_spos, o_sflr, o_inv;
+    size_t o_cpos;  // write stage, vector outputs: positions in cell-list order (over key .. rec)
     size_t o_arr, o_tor, o_rot;  // o_arr: cell-list ids in arrival order (before the in-bin sort)
     size_t o_tcnt, o_tstart, o_wgb;  // tile-level counting sort: tile totals, starts, chunk bases
     size_t o_tarr;                   // the same sort of explicit targets: their tile buckets
@@ -251,6 +252,9 @@ inline void plan_layout(Plan& p)
     p.o_key = take(4 * n);
     p.o_rank = take(4 * n);
     p.o_rec = take(16 * n);
+    // key, rank and rec serve the count stage's sort only; the write stage reuses their
+    // 24 bytes per atom (or more) for the positions in cell-list order
+    p.o_cpos = p.o_key;
     p.o_bcnt = take(4 * nbins);
     p.o_bstart = take(4 * (nbins + 1));
     p.o_sid = take(4 * n);

@@ -15,7 +15,7 @@ from dynamis_amd.dynamis_state import dynamis_state_impl as impl
 pytestmark = pytest.mark.gpu
 
 
-def _one_call(pos, cell, pbc, r, targets, capacity, vdt=None):
+def _one_call(pos, cell, pbc, r, targets, capacity, vdt=None, vec_offset=0):
     lib = L.lib()
     d = impl._desc(pos, cell, pbc, impl._r32(r), targets)
     dev = pos.device
@@ -27,8 +27,9 @@ def _one_call(pos, cell, pbc, r, targets, capacity, vdt=None):
     sh = torch.full((capacity, 3), -7.0, dtype=torch.float32, device=dev)
     vec = dist = None
     if vdt is not None:
-        vec = torch.empty((capacity, 3), dtype=vdt, device=dev)
-        dist = torch.empty(capacity, dtype=vdt, device=dev)
+        # vec_offset elements in: outputs off the 16-byte alignment the grouped stores need
+        vec = torch.empty(3 * capacity + vec_offset, dtype=vdt, device=dev)[vec_offset:].view(capacity, 3)
+        dist = torch.empty(capacity + vec_offset, dtype=vdt, device=dev)[vec_offset:]
     s = L.stream_of(dev)
     st = lib.dg_graph_build(d, L.ptr(pos), L.ptr(targets), L.ptr(ws), wsb, capacity, L.ptr(cnt),
                             L.ctypes.c_void_p(ei.data_ptr()),
@@ -102,3 +103,29 @@ def test_capacity_too_small_reports_count(cuda):
     st, E1, ei1, _, _, _, _ = _one_call(p, c, bb, b.radius, None, E // 2)
     assert st == L.DG_ERR_CAPACITY and E1 == E
     assert "capacity" in L.lib().dg_last_error().decode()
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: c[0])
+def test_vectors_grouped_equal_per_lane(cuda, case):
+    """Edge vectors and distances written in 16-byte groups (outputs aligned to 16 bytes)
+    must be the bytes the per-lane writer gives (outputs one element off that alignment),
+    for fp32 and fp64 vectors, with the edges themselves unchanged."""
+    name, pos, cell, pbc, r, tg = case
+    p = torch.from_numpy(np.ascontiguousarray(pos)).to(cuda)
+    c = torch.from_numpy(np.asarray(cell, np.float64))
+    b = torch.tensor([bool(x) for x in pbc])
+    t = None if tg is None else torch.from_numpy(np.asarray(tg, np.int64)).to(cuda)
+    ei, co, nn, cnt = impl.radius_graph_pbc_ex(p, c, b, r, 0, False, t)
+    E = ei.shape[1]
+    for vdt in (torch.float32, torch.float64):
+        print(f"\n[case] vectors {name} N={len(pos)} {vdt}", flush=True)
+        st, E1, ei1, sh1, _, vec1, dist1 = _one_call(p, c, b, r, t, E + 3, vdt)
+        st2, E2, ei2, sh2, _, vec2, dist2 = _one_call(p, c, b, r, t, E + 3, vdt, vec_offset=1)
+        assert st == st2 == L.DG_OK and E1 == E2 == E
+        assert vec1.data_ptr() % 16 == 0 and vec2.data_ptr() % 16 != 0
+        assert torch.equal(ei1[:, :E], ei) and torch.equal(sh1[:E], co)
+        assert torch.equal(ei2[:, :E], ei) and torch.equal(sh2[:E], co)
+        assert torch.equal(vec1[:E], vec2[:E]) and torch.equal(dist1[:E], dist2[:E])
+        # and the vectors are the edges' own (|v| = dist, |v| <= r)
+        assert torch.allclose(vec1[:E].double().norm(dim=1), dist1[:E].double(), rtol=1e-6, atol=0)
+        assert float(dist1[:E].max()) <= float(np.float32(r)) * (1 + 1e-6)
