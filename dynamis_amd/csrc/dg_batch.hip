@@ -33,8 +33,8 @@ inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
 inline unsigned nblk(int64_t n, int b = 256) { return (unsigned)((n + b - 1) / b); }
 
 // Per structure, set up on the device from its cell: the cell and its inverse, the
-// periodic image range (|image| <= ceil(r / face distance) + 1 per periodic axis), and the
-// structure's first atom.
+// fractional reach of the cutoff per axis (which bounds each pair's periodic images), and
+// the structure's atom range.
 struct Image {
     double C[9], Cinv[9];
     double cf[3];  // r / face distance: the fractional reach of the cutoff sphere per axis
@@ -126,6 +126,8 @@ __global__ void setup_kernel(int64_t B, int64_t N, const double* __restrict__ ce
     }
     m.off = off[b];
     m.n = natoms[b];
+    // a cell far thinner than the radius is refused, as by the single-structure plan
+    if (m.ok && !(pair_images(m.cf, pbc) <= kMaxPairImages)) m.ok = 0;
     if (!m.ok || m.n < 0) atomicOr((unsigned long long*)&totals[1], (unsigned long long)kStatusRange);
     img[b] = m;
 }
@@ -230,11 +232,12 @@ __global__ __launch_bounds__(256) void batch_kernel(Args a)
     }
 }
 
-__global__ void per_image_kernel(int64_t B, const int64_t* __restrict__ off, const int64_t* __restrict__ offs,
-                                 int64_t* __restrict__ out)
+__global__ void per_image_kernel(int64_t B, int64_t N, const int64_t* __restrict__ off,
+                                 const int64_t* __restrict__ offs, int64_t* __restrict__ out)
 {
     const int64_t b = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (b < B) out[b] = offs[off[b + 1]] - offs[off[b]];
+    // (atom counts that do not add up, flagged by setup_kernel, must not index past offs)
+    if (b < B) out[b] = offs[min(max(off[b + 1], (int64_t)0), N)] - offs[min(max(off[b], (int64_t)0), N)];
 }
 
 dg_status check(const dg_batch_desc* d)
@@ -326,7 +329,10 @@ dg_status dg_batch_read_totals(const dg_batch_desc* desc, const void* ws, int64_
     if (total_edges) *total_edges = h[0];
     if (flags) *flags = h[1];
     if (h[1] & kStatusNonFinite) return fail(DG_ERR_RANGE, "pos contains non-finite values");
-    if (h[1] & kStatusRange) return fail(DG_ERR_INVALID, "a cell is singular, or the atom counts are negative or do not add up to n_atoms");
+    if (h[1] & kStatusRange)
+        return fail(DG_ERR_INVALID, "a cell is singular or too thin for the radius (more than 2^24 periodic "
+                                    "images per atom pair), or the atom counts are negative or do not add "
+                                    "up to n_atoms");
     if (h[1] & kStatusCapacity) return fail(DG_ERR_CAPACITY, "edge capacity exceeded");
     return DG_OK;
 }
@@ -352,7 +358,8 @@ dg_status dg_batch_write(const dg_batch_desc* desc, const void* pos, void* ws, s
     if (edges_per_image) {
         char* w = (char*)ws;
         hipLaunchKernelGGL(per_image_kernel, dim3(nblk(desc->n_images)), dim3(256), 0, s, desc->n_images,
-                           (const int64_t*)(w + L.o_off), (const int64_t*)(w + L.o_offs), edges_per_image);
+                           desc->n_atoms, (const int64_t*)(w + L.o_off), (const int64_t*)(w + L.o_offs),
+                           edges_per_image);
     }
     return launched("dg_batch_write");
 }

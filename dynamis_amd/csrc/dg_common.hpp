@@ -26,6 +26,20 @@ constexpr int kStatusRange = 1;     // an atom lies more than kFloorMax cells ou
 constexpr int kStatusNonFinite = 2; // NaN / inf position
 constexpr int kStatusCapacity = 4;  // edge output capacity exceeded
 
+// Periodic images that one atom pair may have within the cutoff, at most: a cell far
+// thinner than the radius is refused (the all-pairs kernels loop over these images per pair;
+// the reference materialises n (2 ceil(cf) + 1)^3 image atoms for it and runs out of memory).
+constexpr double kMaxPairImages = 16777216.0;  // 2^24
+
+// Upper bound on the images per atom pair: every shift S with |x - S| <= cf on a periodic
+// axis (cf = r / face distance), one on the others.
+DG_HD double pair_images(const double* cf, const int* pbc)
+{
+    double m = 1.0;
+    for (int d = 0; d < 3; ++d) m *= pbc[d] ? 2.0 * cf[d] + 1.0 : 1.0;
+    return m;
+}
+
 DG_HD double canon_frac(double p0, double p1, double p2, const double* Cinv, int j)
 {
     return fma(p2, Cinv[6 + j], fma(p1, Cinv[3 + j], p0 * Cinv[j]));

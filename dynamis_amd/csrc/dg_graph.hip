@@ -1980,6 +1980,8 @@ dg_status make_plan(const dg_graph_desc* d, Plan& p)
     p.nt = d->has_targets ? d->n_targets : d->n_atoms;
     p.f64 = d->pos_dtype == DG_F64;
     if (plan_geometry(p, d->cell, d->pbc, d->radius)) return fail(DG_ERR_INVALID, "cell is singular");
+    if (!(pair_images(p.cf, p.pbc) <= kMaxPairImages))
+        return fail(DG_ERR_INVALID, "cell too thin for the radius: more than 2^24 periodic images per atom pair");
     plan_grid(p);
     plan_layout(p);
     if (p.nbins >= 0x7fffffffLL || p.ncodes >= 0x7fffffffLL)

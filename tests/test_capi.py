@@ -47,6 +47,9 @@ def test_workspace_size_and_validation():
     assert b"radius must be positive" in lib.dg_last_error()
     assert lib.dg_graph_workspace_size(_desc(10, cell=np.zeros((3, 3)))) == 0
     assert b"singular" in lib.dg_last_error()
+    # a cell far thinner than the radius (2 r / 1e-7 images per pair on one axis) is refused
+    assert lib.dg_graph_workspace_size(_desc(10, cell=np.diag([10.0, 10.0, 1e-7]))) == 0
+    assert b"too thin" in lib.dg_last_error()
     # a workspace that is too small is refused before anything is launched
     d = _desc(100)
     st = lib.dg_graph_count(d, ctypes.c_void_p(1), None, ctypes.c_void_p(1), 16, None, None)

@@ -114,6 +114,10 @@ def test_batch_errors(cuda):
     sing[1] = 0.0
     with pytest.raises(RuntimeError, match="singular"):
         impl.build_batch(p, torch.from_numpy(sing), torch.from_numpy(natoms), torch.tensor(pbc), r)
+    thin = cells.copy()
+    thin[2] = np.diag([10.0, 10.0, 1e-7])  # 1.2e8 periodic images per pair on one axis
+    with pytest.raises(RuntimeError, match="too thin"):
+        impl.build_batch(p, torch.from_numpy(thin), torch.from_numpy(natoms), torch.tensor([True] * 3), r)
     # a good batch right after
     ei, co, nn = impl.build_batch(p, torch.from_numpy(cells), torch.from_numpy(natoms), torch.tensor(pbc), r)
     assert int(nn.sum()) == ei.shape[1]
