@@ -3,7 +3,8 @@ per-target counts after the canonical sort): random cells (cubic, orthorhombic,
 lower-triangular, general, thin slabs), PBC patterns, radii from below one bin to several
 cell widths, fp32 and fp64 positions, positions inside and outside the cell, atom counts
 from 1 to tens of thousands, with and without explicit targets (prefix, random subsets
-with duplicates).  Each case prints its parameters before it runs."""
+with duplicates); edge vectors and distances on a quarter of the cases.  Each case prints
+its parameters before it runs."""
 import numpy as np
 import pytest
 import torch
@@ -106,3 +107,35 @@ def test_random_all_pairs(cuda, seed):
     want = oracle.canonical_sort(o["src"], o["dst"], o["shift"])
     for a, b in zip(got, want):
         assert np.array_equal(a, b)
+
+
+@pytest.mark.parametrize("seed", range(40))
+def test_random_vectors(cuda, seed):
+    """Edge vectors and distances on the sweep's cases (every fourth seed, so every cell
+    kind, PBC pattern, target kind and position dtype comes up), fp32 and fp64 vectors in
+    turn: fp64 bit-identical to the canonical formula, fp32 its rounding, distances within
+    1e-15 relative (fp64) or 2 ulp (fp32) of the oracle's."""
+    kind, cell, pbc, r, pos, tg = _case(4 * seed + seed % 4)
+    vdt = torch.float64 if seed % 2 else torch.float32
+    print(f"\n[case] random vectors seed={seed} kind={kind} n={len(pos)} dtype={pos.dtype} pbc={pbc} "
+          f"r={r:.3f} targets={None if tg is None else len(tg)} vectors={vdt}", flush=True)
+    pt = torch.from_numpy(np.ascontiguousarray(pos)).to(cuda)
+    tt = None if tg is None else torch.from_numpy(tg).to(cuda)
+    ei, co, nn, cnt, vec, dist = impl.radius_graph_pbc_vectors(pt, torch.from_numpy(cell), torch.tensor(pbc), r,
+                                                               tt, vector_dtype=vdt)
+    cell_used = np.asarray(cell, np.float64).astype(pos.dtype).astype(np.float64)
+    o = oracle.radius_graph(pos, cell_used, pbc, float(np.float32(r)), target_indices=tg, vectors=True)
+    assert ei.shape[1] == len(o["src"]) == int(nn.item())
+    assert np.array_equal(cnt.cpu().numpy(), o["counts"])
+    got = oracle.canonical_sort(ei[0].cpu().numpy(), ei[1].cpu().numpy(), co.cpu().numpy().astype(np.int64),
+                                vec.cpu().numpy(), dist.cpu().numpy())
+    want = oracle.canonical_sort(o["src"], o["dst"], o["shift"], o["vec"], np.sqrt(o["d2"]))
+    for a, b in zip(got[:3], want[:3]):
+        assert np.array_equal(a, b)
+    if vdt == torch.float64:
+        assert np.array_equal(got[3], want[3])
+        assert np.allclose(got[4], want[4], rtol=1e-15, atol=0)
+    else:
+        assert np.array_equal(got[3], want[3].astype(np.float32))
+        ulp = np.spacing(want[4].astype(np.float32))
+        assert np.all(np.abs(got[4].astype(np.float64) - want[4]) <= 2 * ulp)
