@@ -1786,8 +1786,9 @@ __global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
 
 // ---------------------------------------------------------------- all-pairs fallback
 // Used only when the search region of a tile would exceed kMaxRegion bins (cutoff much
-// larger than the cell).  One thread per target, every atom, every periodic image in
-// |S_d| <= ceil(cutoff_frac_d) + 1.
+// larger than the cell).  One thread per target, every atom, and for each pair every
+// periodic shift that can put the source within the cutoff (brute_kernel: the exact
+// per-pair range).
 struct BruteArgs {
     double C[9], Cinv[9];
     double r2;
