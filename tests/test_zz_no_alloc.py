@@ -1,5 +1,6 @@
 """dg_graph_build_noalloc (the allocation-free build, C ABI) against dg_graph_build with a
-caller workspace: byte-identical edges, shifts and counts, and the same {edge count,
+caller workspace: byte-identical edges, shifts, counts (and edge vectors and distances),
+and the same {edge count,
 flags}, on two calls in a row -- the second on a smaller input, so stale contents of the
 shared static scratch from the first call would show -- and a build too large for the
 scratch is refused before anything runs."""
@@ -29,33 +30,46 @@ def _outputs(cap, nt, dev):
     return ei, sh, cnt
 
 
-def _with_workspace(box, dev, cap):
+def _vec_outputs(cap, dev, vectors):
+    if not vectors:
+        return None, None
+    return (torch.full((cap, 3), -7.0, dtype=torch.float32, device=dev),
+            torch.full((cap,), -7.0, dtype=torch.float32, device=dev))
+
+
+def _with_workspace(box, dev, cap, vectors=False):
     lib = L.lib()
     d, pos, tgt = _desc(box, dev)
     wsb = lib.dg_graph_workspace_size(d)
     ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
     ei, sh, cnt = _outputs(cap, pos.shape[0] if tgt is None else tgt.shape[0], dev)
+    vec, dist = _vec_outputs(cap, dev, vectors)
     s = L.stream_of(dev)
     L.check(lib.dg_graph_build(d, L.ptr(pos), L.ptr(tgt), L.ptr(ws), wsb, cap, L.ptr(cnt),
                                L.ctypes.c_void_p(ei.data_ptr()), L.ctypes.c_void_p(ei.data_ptr() + 8 * cap),
-                               L.ptr(sh), None, None, L.DG_F32, s), "dg_graph_build")
+                               L.ptr(sh), L.ptr(vec), L.ptr(dist), L.DG_F32, s), "dg_graph_build")
     E, fl = L._i64(0), L._i64(0)
     L.check(lib.dg_graph_read_totals(d, L.ptr(ws), E, fl, s), "totals")
+    if vectors:
+        return int(E.value), int(fl.value), ei, sh, cnt, vec, dist
     return int(E.value), int(fl.value), ei, sh, cnt
 
 
-def _no_alloc(box, dev, cap):
+def _no_alloc(box, dev, cap, vectors=False):
     lib = L.lib()
     d, pos, tgt = _desc(box, dev)
     ei, sh, cnt = _outputs(cap, pos.shape[0] if tgt is None else tgt.shape[0], dev)
+    vec, dist = _vec_outputs(cap, dev, vectors)
     tot = torch.full((2,), -7, dtype=torch.int64, device=dev)
     s = L.stream_of(dev)
     L.check(lib.dg_graph_build_noalloc(d, L.ptr(pos), L.ptr(tgt), cap, L.ptr(cnt),
                                        L.ctypes.c_void_p(ei.data_ptr()),
-                                       L.ctypes.c_void_p(ei.data_ptr() + 8 * cap), L.ptr(sh), None,
-                                       None, L.DG_F32, L.ptr(tot), s), "dg_graph_build_noalloc")
+                                       L.ctypes.c_void_p(ei.data_ptr() + 8 * cap), L.ptr(sh), L.ptr(vec),
+                                       L.ptr(dist), L.DG_F32, L.ptr(tot), s), "dg_graph_build_noalloc")
     torch.cuda.synchronize()
     t = tot.cpu().tolist()
+    if vectors:
+        return int(t[0]), int(t[1]), ei, sh, cnt, vec, dist
     return int(t[0]), int(t[1]), ei, sh, cnt
 
 
@@ -75,6 +89,22 @@ def test_no_alloc_matches_workspace_build(cuda):
         assert torch.equal(ei2[:, :E], ei[:, :E])
         assert torch.equal(sh2[:E], sh[:E])
         assert bool((ei2[:, E:] == -7).all())  # nothing written past the edges
+
+
+def test_no_alloc_vectors(cuda):
+    # edge vectors and distances too (their cell-ordered positions live in the scratch):
+    # two calls in a row, the second smaller
+    for name, box in [("uniform 40000", configs.uniform(40000, seed=33, dtype=np.float32)),
+                      ("uniform 7000", configs.uniform(7000, seed=34, dtype=np.float32))]:
+        print(f"\n[case] noalloc vectors {name} N={len(box.pos)}", flush=True)
+        E, *_ = _with_workspace(box, cuda, int(len(box.pos) * 100))
+        cap = E + 64
+        E, fl, ei, sh, cnt, vec, dist = _with_workspace(box, cuda, cap, vectors=True)
+        E2, fl2, ei2, sh2, cnt2, vec2, dist2 = _no_alloc(box, cuda, cap, vectors=True)
+        assert (E2, fl2) == (E, fl) and E > 0
+        assert torch.equal(cnt2, cnt) and torch.equal(ei2[:, :E], ei[:, :E]) and torch.equal(sh2[:E], sh[:E])
+        assert torch.equal(vec2[:E], vec[:E]) and torch.equal(dist2[:E], dist[:E])
+        assert bool((vec2[E:] == -7.0).all()) and bool((dist2[E:] == -7.0).all())
 
 
 def test_no_alloc_capacity_and_limit(cuda):
