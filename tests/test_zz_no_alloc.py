@@ -1,9 +1,8 @@
 """dg_graph_build_noalloc (the allocation-free build, C ABI) against dg_graph_build with a
 caller workspace: byte-identical edges, shifts, counts (and edge vectors and distances),
 and the same {edge count, flags}, on two calls in a row -- the second on a smaller input,
-so stale contents of the
-shared static scratch from the first call would show -- and a build too large for the
-scratch is refused before anything runs."""
+so stale contents of the shared static scratch from the first call would show -- and a
+build too large for the scratch is refused before anything runs."""
 import numpy as np
 import pytest
 import torch
