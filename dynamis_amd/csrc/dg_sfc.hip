@@ -16,6 +16,7 @@
 
 #include <algorithm>
 #include <string>
+#include <vector>
 
 #include "../../include/dynamis_graph.h"
 #include "dg_common.hpp"
@@ -29,9 +30,6 @@ dg_status fail(dg_status st, const std::string& msg);
 namespace {
 using namespace dg;
 
-constexpr int kRsBlock = 256;
-constexpr int kRsRounds = 4;
-constexpr int kRsTile = kRsBlock * kRsRounds;  // keys per workgroup per pass
 
 inline size_t al(size_t x) { return (x + 255) & ~(size_t)255; }
 inline unsigned nblk(int64_t n, int b = 256) { return (unsigned)((n + b - 1) / b); }
@@ -147,19 +145,35 @@ __global__ void keys_kernel(const float* __restrict__ pos, int64_t n, int curve,
 }
 
 // ------------------------------------------------------------------ radix sort
-// OR / AND of all keys tell which bytes vary.
-__global__ void key_span_kernel(const int64_t* __restrict__ keys, int64_t n,
-                                unsigned long long* __restrict__ span)
+// Stable LSD radix sort, 8 bits per pass, with passes only over the key bytes that vary
+// (the OR and AND of all keys, folded per workgroup on the device and across workgroups
+// on the host).  Per pass: rs_hist_kernel counts each tile's digits (digit-major,
+// hist[d * nblocks + b]); a scan of those counts gives every tile its place within every
+// digit; rs_scatter_kernel ranks its tile's keys stably (index order within a digit),
+// reorders them by digit in LDS and writes each digit's run contiguously, keys and then
+// positions.  Keys are kept with the sign bit flipped between passes (so they order as
+// unsigned); positions are int32 inside the sort, and the last pass writes them into the
+// int64 permutation.
+constexpr int kRsBlock = 256;
+constexpr int kRsPer = 16;                     // keys per thread
+constexpr int kRsTile = kRsBlock * kRsPer;     // keys per tile
+constexpr int kRsWaveKeys = 64 * kRsPer;       // a wave's contiguous share of a tile
+constexpr int kSpanBlocks = 512;               // workgroups of the key span
+
+__device__ __forceinline__ uint64_t ukey(int64_t k) { return (uint64_t)k ^ 0x8000000000000000ull; }
+__device__ __forceinline__ int digit_of(uint64_t k, int shift) { return (int)((k >> shift) & 0xffu); }
+
+// OR and AND of the (sign-flipped) keys: one pair per workgroup, folded on the host
+__global__ __launch_bounds__(256) void key_span_kernel(const int64_t* __restrict__ keys, int64_t n,
+                                                       unsigned long long* __restrict__ part)
 {
     unsigned long long o = 0, a = ~0ull;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
          i += (int64_t)gridDim.x * blockDim.x) {
-        unsigned long long k = (unsigned long long)keys[i] ^ 0x8000000000000000ull;
+        const unsigned long long k = ukey(keys[i]);
         o |= k;
         a &= k;
     }
-    // fold the workgroup's values first: one pair of device atomics per workgroup (atomics
-    // on one address serialise: one pair per wave of a 1M-key launch took 97 us)
     for (int m = 32; m > 0; m >>= 1) {
         o |= (unsigned long long)__shfl_xor((long long)o, m, 64);
         a &= (unsigned long long)__shfl_xor((long long)a, m, 64);
@@ -175,83 +189,145 @@ __global__ void key_span_kernel(const int64_t* __restrict__ keys, int64_t n,
             o |= s_o[w];
             a &= s_a[w];
         }
-        atomicOr(&span[0], o);
-        atomicAnd(&span[1], a);
+        part[2 * blockIdx.x] = o;
+        part[2 * blockIdx.x + 1] = a;
     }
 }
 
-__global__ void span_init_kernel(unsigned long long* span)
+// FIRST: the caller's keys (signed); later passes read sign-flipped keys.
+template <bool FIRST>
+__device__ __forceinline__ uint64_t load_key(const int64_t* kin, int64_t i)
 {
-    if (threadIdx.x == 0) { span[0] = 0; span[1] = ~0ull; }
+    return FIRST ? ukey(kin[i]) : (uint64_t)kin[i];
 }
 
-__device__ __forceinline__ int digit_of(int64_t k, int shift)
-{
-    return (int)((((unsigned long long)k ^ 0x8000000000000000ull) >> shift) & 0xffu);
-}
-
-// Per-workgroup digit histogram, stored digit-major: hist[d * nblocks + b].
-__global__ __launch_bounds__(kRsBlock) void rs_hist_kernel(const int64_t* __restrict__ keys,
-                                                           int64_t n, int shift,
-                                                           int* __restrict__ hist, int nblocks)
+// Digit counts of every tile of kRsTile keys, stored digit-major: hist[d * nblocks + b].
+// (One-workgroup scans of these counts -- the last workgroup to finish walking the digit
+// columns -- measured 5x slower than the three-kernel device scan: the walk is latency-bound.)
+template <bool FIRST>
+__global__ __launch_bounds__(kRsBlock) void rs_hist_kernel(const int64_t* __restrict__ kin, int64_t n,
+                                                           int shift, int* __restrict__ hist, int nblocks)
 {
     __shared__ int h[256];
     h[threadIdx.x] = 0;
     __syncthreads();
-    int64_t base = (int64_t)blockIdx.x * kRsTile;
-    for (int r = 0; r < kRsRounds; ++r) {
-        int64_t i = base + r * kRsBlock + threadIdx.x;
-        if (i < n) atomicAdd(&h[digit_of(keys[i], shift)], 1);
+    const int64_t base = (int64_t)blockIdx.x * kRsTile;
+#pragma unroll 4
+    for (int u = 0; u < kRsPer; ++u) {
+        const int64_t i = base + u * kRsBlock + threadIdx.x;
+        if (i < n) atomicAdd(&h[digit_of(load_key<FIRST>(kin, i), shift)], 1);
     }
     __syncthreads();
     hist[threadIdx.x * nblocks + blockIdx.x] = h[threadIdx.x];
 }
 
-// Stable scatter: items are ranked in index order within the workgroup (round by round,
-// wave by wave, lane by lane) using ballot match masks.
+struct RsScatterLds {
+    union {
+        uint64_t k[kRsTile];  // the tile's keys in slot (digit) order
+        int32_t v[kRsTile];   // then their positions
+    } buf;
+    uint8_t dig[kRsTile];      // the digit of every slot
+    int start[256];            // first slot of each digit
+    int glob[256];             // output index of slot 0 of each digit's run, for this tile
+    int wc[kRsBlock / 64][256];  // per wave: running count per digit, then its first slot
+    int w32[kRsBlock / 64];
+};
+
+// One tile: stable slots by digit (wave w holds keys [w kRsWaveKeys, (w + 1) kRsWaveKeys)
+// of the tile, 64 per round; a key's rank among its wave's equal digits comes from eight
+// ballots per round and the wave's running count), then the reorder through LDS and the
+// contiguous write of every digit's run.  FIRST: positions are the keys' indices; LAST:
+// positions go to perm (int64) and the keys are not written.
+template <bool FIRST, bool LAST>
 __global__ __launch_bounds__(kRsBlock) void rs_scatter_kernel(
-    const int64_t* __restrict__ kin, const int64_t* __restrict__ vin, int64_t n, int shift,
-    const int* __restrict__ offs, int nblocks, int64_t* __restrict__ kout, int64_t* __restrict__ vout)
+    const int64_t* __restrict__ kin, const int32_t* __restrict__ vin, int64_t n, int shift,
+    const int* __restrict__ offs, int nblocks, int64_t* __restrict__ kout, int32_t* __restrict__ vout,
+    int64_t* __restrict__ perm)
 {
-    __shared__ int run[256];
-    __shared__ int wc[kRsBlock / 64][256];
+    __shared__ RsScatterLds S;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    run[threadIdx.x] = offs[threadIdx.x * nblocks + blockIdx.x];
-    for (int k = 0; k < kRsBlock / 64; ++k) wc[k][threadIdx.x] = 0;
+    const int64_t base = (int64_t)blockIdx.x * kRsTile;
+    const int m = (int)((n - base) < kRsTile ? (n - base) : kRsTile);  // keys in this tile
+    for (int k = 0; k < kRsBlock / 64; ++k) S.wc[k][threadIdx.x] = 0;
     __syncthreads();
-    const uint64_t lt = (lane == 0) ? 0ull : (~0ull >> (64 - lane));
-    int64_t base = (int64_t)blockIdx.x * kRsTile;
-    for (int r = 0; r < kRsRounds; ++r) {
-        int64_t i = base + r * kRsBlock + threadIdx.x;
-        const bool valid = i < n;
-        int64_t k = valid ? kin[i] : 0;
-        int64_t v = valid ? (vin ? vin[i] : i) : 0;
-        int d = valid ? digit_of(k, shift) : 0;
+    uint64_t key[kRsPer];
+    int32_t val[kRsPer];
+    int rk[kRsPer];
+    const uint64_t lt = lane == 0 ? 0ull : (~0ull >> (64 - lane));
+#pragma unroll
+    for (int u = 0; u < kRsPer; ++u) {
+        const int i = w * kRsWaveKeys + u * 64 + lane;
+        const bool valid = i < m;
+        key[u] = valid ? load_key<FIRST>(kin, base + i) : 0ull;
+        val[u] = valid ? (FIRST ? (int32_t)(base + i) : vin[base + i]) : 0;
+    }
+#pragma unroll
+    for (int u = 0; u < kRsPer; ++u) {
+        const int i = w * kRsWaveKeys + u * 64 + lane;
+        const bool valid = i < m;
+        const int d = digit_of(key[u], shift);
         uint64_t match = __ballot(valid);
+#pragma unroll
         for (int bit = 0; bit < 8; ++bit) {
-            uint64_t b = __ballot(valid && ((d >> bit) & 1));
+            const uint64_t b = __ballot(valid && ((d >> bit) & 1));
             match &= ((d >> bit) & 1) ? b : ~b;
         }
-        int inwave = __popcll(match & lt);
-        bool leader = valid && inwave == 0;
-        if (leader) wc[w][d] = __popcll(match);
-        __syncthreads();
-        if (valid) {
-            int pre = run[d];
-            for (int k2 = 0; k2 < w; ++k2) pre += wc[k2][d];
-            int64_t dst = pre + inwave;
-            kout[dst] = k;
-            vout[dst] = v;
+        const int inwave = __popcll(match & lt);
+        const int before = valid ? S.wc[w][d] : 0;  // the wave's earlier keys of digit d
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        if (valid && inwave == 0) S.wc[w][d] = before + __popcll(match);
+        __builtin_amdgcn_fence(__ATOMIC_RELEASE, "wavefront");
+        __builtin_amdgcn_wave_barrier();
+        __builtin_amdgcn_fence(__ATOMIC_ACQUIRE, "wavefront");
+        rk[u] = before + inwave;
+    }
+    __syncthreads();
+    // thread d: the digit's count and start in the tile, each wave's first slot of it, and
+    // where slot 0 of the digit's run lands in the output
+    {
+        const int d = threadIdx.x;
+        int c = 0;
+        for (int k = 0; k < kRsBlock / 64; ++k) c += S.wc[k][d];
+        int tot;
+        const int ex = block_excl_scan<int, kRsBlock>(c, S.w32, &tot);
+        int at = ex;
+        for (int k = 0; k < kRsBlock / 64; ++k) {
+            const int ck = S.wc[k][d];
+            S.wc[k][d] = at;
+            at += ck;
         }
-        __syncthreads();
-        // advance the running offsets and clear the per-wave counts
-        int add = 0;
-        for (int k2 = 0; k2 < kRsBlock / 64; ++k2) {
-            add += wc[k2][threadIdx.x];
-            wc[k2][threadIdx.x] = 0;
+        S.start[d] = ex;
+        S.glob[d] = offs[(int64_t)d * nblocks + blockIdx.x] - ex;
+    }
+    __syncthreads();
+    int slot[kRsPer];
+#pragma unroll
+    for (int u = 0; u < kRsPer; ++u) {
+        const int i = w * kRsWaveKeys + u * 64 + lane;
+        slot[u] = -1;
+        if (i < m) {
+            const int d = digit_of(key[u], shift);
+            slot[u] = S.wc[w][d] + rk[u];
+            S.buf.k[slot[u]] = key[u];
+            S.dig[slot[u]] = (uint8_t)d;
         }
-        run[threadIdx.x] += add;
-        __syncthreads();
+    }
+    __syncthreads();
+    if constexpr (!LAST)
+        for (int sl = threadIdx.x; sl < m; sl += kRsBlock) kout[S.glob[S.dig[sl]] + sl] = (int64_t)S.buf.k[sl];
+    __syncthreads();
+#pragma unroll
+    for (int u = 0; u < kRsPer; ++u)
+        if (slot[u] >= 0) S.buf.v[slot[u]] = val[u];
+    __syncthreads();
+    for (int sl = threadIdx.x; sl < m; sl += kRsBlock) {
+        const int64_t dst = S.glob[S.dig[sl]] + sl;
+        if constexpr (LAST)
+            perm[dst] = (int64_t)S.buf.v[sl];
+        else
+            vout[dst] = S.buf.v[sl];
     }
 }
 
@@ -589,7 +665,7 @@ dg_status launch_ok(const char* what)
 
 struct SortLayout {
     size_t o_k0, o_v0, o_k1, o_v1, o_hist, o_offs, o_part, o_span, total;
-    int nblocks;
+    int nblocks, nspan;
 };
 
 SortLayout sort_layout(int64_t n)
@@ -600,14 +676,15 @@ SortLayout sort_layout(int64_t n)
     L.nblocks = (int)((n + kRsTile - 1) / kRsTile);
     if (L.nblocks < 1) L.nblocks = 1;
     size_t nh = (size_t)L.nblocks * 256;
+    L.nspan = (int)std::min<int64_t>(kSpanBlocks, std::max<int64_t>(1, (n + 255) / 256));
     L.o_k0 = take(8 * n);
-    L.o_v0 = take(8 * n);
+    L.o_v0 = take(4 * n);
     L.o_k1 = take(8 * n);
-    L.o_v1 = take(8 * n);
+    L.o_v1 = take(4 * n);
     L.o_hist = take(4 * nh);
     L.o_offs = take(4 * (nh + 1));
     L.o_part = take(4 * (nh / kScanTile + 2));
-    L.o_span = take(16);
+    L.o_span = take(16 * (size_t)L.nspan);
     L.total = o;
     return L;
 }
@@ -673,40 +750,56 @@ dg_status dg_sfc_order(const int64_t* keys, int64_t n, int64_t* perm, void* ws, 
     if (ws_bytes < L.total) return fail(DG_ERR_WORKSPACE, "workspace too small");
     char* w = (char*)ws;
     unsigned long long* span = (unsigned long long*)(w + L.o_span);
-    hipLaunchKernelGGL(span_init_kernel, dim3(1), dim3(64), 0, s, span);
-    hipLaunchKernelGGL(key_span_kernel, dim3(nblk(n) > 128 ? 128 : nblk(n)), dim3(256), 0, s, keys, n, span);
-    unsigned long long h[2];
-    hipError_t e = hipMemcpyAsync(h, span, sizeof h, hipMemcpyDeviceToHost, s);
+    hipLaunchKernelGGL(key_span_kernel, dim3((unsigned)L.nspan), dim3(256), 0, s, keys, n, span);
+    std::vector<unsigned long long> h(2 * (size_t)L.nspan);
+    hipError_t e = hipMemcpyAsync(h.data(), span, 16 * (size_t)L.nspan, hipMemcpyDeviceToHost, s);
     if (e == hipSuccess) e = hipStreamSynchronize(s);
     if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("dg_sfc_order: ") + hipGetErrorString(e));
-    unsigned long long vary = h[0] & ~h[1];
-    const int64_t* kin = keys;
-    const int64_t* vin = nullptr;
-    int64_t* kb[2] = {(int64_t*)(w + L.o_k0), (int64_t*)(w + L.o_k1)};
-    int64_t* vb[2] = {(int64_t*)(w + L.o_v0), (int64_t*)(w + L.o_v1)};
-    int cur = 0;
-    int passes = 0;
-    for (int shift = 0; shift < 64; shift += 8) {
-        if (((vary >> shift) & 0xffull) == 0) continue;
-        int* hist = (int*)(w + L.o_hist);
-        int* offs = (int*)(w + L.o_offs);
-        int64_t nh = (int64_t)L.nblocks * 256;
-        hipLaunchKernelGGL(rs_hist_kernel, dim3(L.nblocks), dim3(kRsBlock), 0, s, kin, n, shift, hist, L.nblocks);
-        device_excl_scan<int, int>(hist, nh, offs, (int*)(w + L.o_part), s);
-        hipLaunchKernelGGL(rs_scatter_kernel, dim3(L.nblocks), dim3(kRsBlock), 0, s, kin, vin, n, shift,
-                           (const int*)offs, L.nblocks, kb[cur], vb[cur]);
-        kin = kb[cur];
-        vin = vb[cur];
-        cur ^= 1;
-        ++passes;
+    unsigned long long o = 0, a = ~0ull;
+    for (int b = 0; b < L.nspan; ++b) {
+        o |= h[2 * b];
+        a &= h[2 * b + 1];
     }
-    if (passes == 0) {
+    const unsigned long long vary = o & ~a;
+    int shifts[8], npass = 0;
+    for (int sh = 0; sh < 64; sh += 8)
+        if ((vary >> sh) & 0xffull) shifts[npass++] = sh;
+    if (npass == 0) {
         // all keys equal: identity permutation
         hipLaunchKernelGGL(iota_kernel, dim3(nblk(n)), dim3(256), 0, s, n, perm);
         return launch_ok("dg_sfc_order");
     }
-    e = hipMemcpyAsync(perm, vin, 8 * (size_t)n, hipMemcpyDeviceToDevice, s);
-    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("dg_sfc_order: ") + hipGetErrorString(e));
+    int64_t* kb[2] = {(int64_t*)(w + L.o_k0), (int64_t*)(w + L.o_k1)};
+    int32_t* vb[2] = {(int32_t*)(w + L.o_v0), (int32_t*)(w + L.o_v1)};
+    int* hist = (int*)(w + L.o_hist);
+    int* offs = (int*)(w + L.o_offs);
+    const int64_t nh = (int64_t)L.nblocks * 256;
+    const dim3 grid((unsigned)L.nblocks), blk(kRsBlock);
+    for (int q = 0; q < npass; ++q) {
+        const bool first = q == 0, last = q == npass - 1;
+        const int64_t* kin = first ? keys : kb[(q - 1) & 1];
+        const int32_t* vin = first ? nullptr : vb[(q - 1) & 1];
+        int64_t* kout = kb[q & 1];
+        int32_t* vout = vb[q & 1];
+        const int sh = shifts[q];
+        if (first)
+            hipLaunchKernelGGL(rs_hist_kernel<true>, grid, blk, 0, s, kin, n, sh, hist, L.nblocks);
+        else
+            hipLaunchKernelGGL(rs_hist_kernel<false>, grid, blk, 0, s, kin, n, sh, hist, L.nblocks);
+        excl_scan<int, int>(hist, nh, offs, (int*)(w + L.o_part), s);
+        if (first && last)
+            hipLaunchKernelGGL((rs_scatter_kernel<true, true>), grid, blk, 0, s, kin, vin, n, sh,
+                               (const int*)offs, L.nblocks, kout, vout, perm);
+        else if (first)
+            hipLaunchKernelGGL((rs_scatter_kernel<true, false>), grid, blk, 0, s, kin, vin, n, sh,
+                               (const int*)offs, L.nblocks, kout, vout, perm);
+        else if (last)
+            hipLaunchKernelGGL((rs_scatter_kernel<false, true>), grid, blk, 0, s, kin, vin, n, sh,
+                               (const int*)offs, L.nblocks, kout, vout, perm);
+        else
+            hipLaunchKernelGGL((rs_scatter_kernel<false, false>), grid, blk, 0, s, kin, vin, n, sh,
+                               (const int*)offs, L.nblocks, kout, vout, perm);
+    }
     return launch_ok("dg_sfc_order");
 }
 
