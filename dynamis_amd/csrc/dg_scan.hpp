@@ -9,6 +9,7 @@ constexpr int kScanBlock = 256;
 constexpr int kScanItems = 8;
 constexpr int kScanTile = kScanBlock * kScanItems;  // 2048 items per workgroup
 constexpr int kSmallScanBlock = 1024;  // the one-workgroup scan of short arrays
+constexpr int64_t kScanSumParts = 1024;  // up to this many tiles the last phase sums the partials
 
 // Inclusive scan across one wave64.
 template <typename T>
@@ -94,13 +95,23 @@ __global__ __launch_bounds__(kScanBlock) void scan_partials_kernel(Tout* __restr
 }
 
 // Phase 3: exclusive scan of each tile plus its offset; out has n+1 entries, out[n] = sum.
-template <typename Tin, typename Tout>
+// SUM_PARTS: part holds the per-tile sums unscanned, and each workgroup adds up those before
+// it (few tiles: phase 2's launch saved).
+template <typename Tin, typename Tout, bool SUM_PARTS = false>
 __global__ __launch_bounds__(kScanBlock) void scan_final_kernel(const Tin* __restrict__ in,
                                                                 int64_t n,
                                                                 const Tout* __restrict__ part,
                                                                 Tout* __restrict__ out)
 {
     __shared__ Tout s_w[kScanBlock / 64];
+    Tout off;
+    if constexpr (SUM_PARTS) {
+        Tout p = 0;
+        for (int i = threadIdx.x; i < (int)blockIdx.x; i += kScanBlock) p += part[i];
+        block_excl_scan<Tout, kScanBlock>(p, s_w, &off);
+    } else {
+        off = part[blockIdx.x];
+    }
     int64_t base = (int64_t)blockIdx.x * kScanTile + (int64_t)threadIdx.x * kScanItems;
     Tout v[kScanItems];
     Tout s = 0;
@@ -110,7 +121,7 @@ __global__ __launch_bounds__(kScanBlock) void scan_final_kernel(const Tin* __res
         s += v[k];
     }
     Tout tot;
-    Tout ex = block_excl_scan<Tout, kScanBlock>(s, s_w, &tot) + part[blockIdx.x];
+    Tout ex = block_excl_scan<Tout, kScanBlock>(s, s_w, &tot) + off;
 #pragma unroll
     for (int k = 0; k < kScanItems; ++k) {
         if (base + k < n) out[base + k] = ex;
@@ -127,6 +138,11 @@ inline void device_excl_scan(const Tin* in, int64_t n, Tout* out, Tout* part, hi
     int64_t nblk = n / kScanTile + 1;
     hipLaunchKernelGGL((scan_reduce_kernel<Tin, Tout>), dim3((unsigned)nblk), dim3(kScanBlock), 0,
                        s, in, n, part);
+    if (nblk <= kScanSumParts) {
+        hipLaunchKernelGGL((scan_final_kernel<Tin, Tout, true>), dim3((unsigned)nblk), dim3(kScanBlock), 0,
+                           s, in, n, (const Tout*)part, out);
+        return;
+    }
     hipLaunchKernelGGL((scan_partials_kernel<Tout>), dim3(1), dim3(kScanBlock), 0, s, part, nblk);
     hipLaunchKernelGGL((scan_final_kernel<Tin, Tout>), dim3((unsigned)nblk), dim3(kScanBlock), 0,
                        s, in, n, part, out);
