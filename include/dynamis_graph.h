@@ -95,7 +95,11 @@ dg_status dg_graph_read_totals(const dg_graph_desc* desc, const void* workspace,
  *   edge_dist            device [capacity] of vec_dtype or NULL (sqrt(d2))
  * Edges are grouped by target in the SFC processing order; within a target the order
  * is fixed (deterministic) but unspecified.  Tiles that would overrun `capacity` are
- * skipped and DG_FLAG_CAPACITY is raised. */
+ * skipped and DG_FLAG_CAPACITY is raised.  Outputs aligned to 16 bytes are written in
+ * 16-byte groups (the fast path; torch allocations are); other alignments give the same
+ * bytes, more slowly.  With edge_vec or edge_dist, the stage reuses the count stage's
+ * sort scratch in the workspace (a later dg_graph_write on the same workspace is still
+ * valid; the count's results it needs are kept). */
 dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
                          void* workspace, size_t workspace_bytes, int64_t capacity,
                          int64_t* edge_src, int64_t* edge_dst, float* cell_shift, void* edge_vec,
