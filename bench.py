@@ -47,12 +47,13 @@ def main():
     ap.add_argument("--vectors", action="store_true",
                     help="graph path: also emit the edge vectors (fp32 [E,3]) and distances "
                          "(fp32 [E]) in the write stage: 44 bytes per edge instead of 28")
-    ap.add_argument("--path", default="graph", choices=["graph", "halo", "filter", "batch"],
+    ap.add_argument("--path", default="graph", choices=["graph", "halo", "filter", "batch", "sfc"],
                     help="graph: the headline full rebuild; halo: extract_halo_info of one rank "
                          "of an 8-way SFC partition of the same box (edges at r + 0.5); filter: "
                          "filter_edges_to_radius of the box's edges at r + 0.5 down to r; batch: "
                          "radius_graph_pbc_cuda on batches of small structures, batched against "
-                         "the per-structure loop")
+                         "the per-structure loop; sfc: the SFC partition of the box's atoms "
+                         "(keys, stable order, labels)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -85,6 +86,8 @@ def main():
         return bench_filter(args)
     if args.path == "batch":
         return bench_batch(args)
+    if args.path == "sfc":
+        return bench_sfc(args)
 
     box = {"C1": configs.fcc, "C2": configs.c2, "C3": configs.c3, "C4": configs.c4,
            "C4-500k": lambda: configs.c4(scale=1.3934), "C5": configs.c5}[args.config]()
@@ -542,6 +545,99 @@ def bench_halo(args):
         "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "dg_halo_count + dg_halo_write (all kernels)", "algorithmic_bytes": nbytes},
+        "cpu_baseline": cpu}), flush=True)
+
+
+def bench_sfc(args):
+    """The SFC partition path (rows a13, a14, f2) on the config's atoms: one step = Morton
+    keys, their stable order and the W = 8 partition labels, through the C ABI into
+    preallocated outputs; each stage is timed with HIP events as well.  The dominant kernel
+    is the sort, whose algorithmic bytes are 16 per key (keys read, permutation written)."""
+    import numpy as np
+    import torch
+
+    from dynamis_amd import _lib as L
+    from dynamis_amd import configs
+
+    W = 8
+    box = {"C2": configs.c2, "C3": configs.c3}[args.config]()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    lib = L.lib()
+    pos = torch.from_numpy(np.ascontiguousarray(box.pos, dtype=np.float32)).to(dev)
+    n = pos.shape[0]
+    wsb = lib.dg_sfc_workspace_size(n)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    keys = torch.empty(n, dtype=torch.int64, device=dev)
+    perm = torch.empty(n, dtype=torch.int64, device=dev)
+    labels = torch.empty(n, dtype=torch.int64, device=dev)
+    weights = torch.from_numpy(np.random.default_rng(3).integers(1, 100, n)).to(dev)
+    s = L.stream_of(dev)
+    stream = torch.cuda.current_stream(dev)
+    ev = [torch.cuda.Event(enable_timing=True) for _ in range(4 * args.steps + 2)]
+
+    def step(k=None):
+        if k is not None:
+            ev[4 * k].record(stream)
+        L.check(lib.dg_sfc_keys(L.ptr(pos), n, 0, L.ptr(keys), L.ptr(ws), wsb, s), "keys")
+        if k is not None:
+            ev[4 * k + 1].record(stream)
+        L.check(lib.dg_sfc_order(L.ptr(keys), n, L.ptr(perm), L.ptr(ws), wsb, s), "order")
+        if k is not None:
+            ev[4 * k + 2].record(stream)
+        L.check(lib.dg_sfc_labels(L.ptr(perm), n, W, None, L.ptr(labels), L.ptr(ws), wsb, s), "labels")
+        if k is not None:
+            ev[4 * k + 3].record(stream)
+
+    for _ in range(args.warmup):
+        step()
+    torch.cuda.synchronize()
+    t0, t1 = ev[-2], ev[-1]
+    t0.record(stream)
+    for k in range(args.steps):
+        step(k)
+    t1.record(stream)
+    torch.cuda.synchronize()
+    ms = t0.elapsed_time(t1) / args.steps
+    st = np.array([[ev[4 * k + j].elapsed_time(ev[4 * k + j + 1]) for j in range(3)] for k in range(args.steps)])
+    keys_ms, order_ms, labels_ms = (float(np.mean(st[:, j])) for j in range(3))
+    # weighted labels (exact int64 cut), timed apart
+    for _ in range(2):
+        L.check(lib.dg_sfc_labels(L.ptr(perm), n, W, L.ptr(weights), L.ptr(labels), L.ptr(ws), wsb, s), "w")
+    a, b = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+    a.record(stream)
+    for _ in range(args.steps):
+        L.check(lib.dg_sfc_labels(L.ptr(perm), n, W, L.ptr(weights), L.ptr(labels), L.ptr(ws), wsb, s), "w")
+    b.record(stream)
+    torch.cuda.synchronize()
+    wlabels_ms = a.elapsed_time(b) / args.steps
+    kbytes = 16 * n
+    ach = kbytes / (order_ms * 1e-3) / 1e9
+    cpu = None
+    if not args.no_cpu:
+        import oracle
+
+        p_np = np.ascontiguousarray(box.pos, dtype=np.float32)
+        tc = time.perf_counter()
+        k_np = oracle.morton_keys(p_np, threads=0)
+        perm_np = np.argsort(k_np, kind="stable")
+        oracle.sfc_labels(perm_np, W)
+        cs = time.perf_counter() - tc
+        cpu = {"value": round(cs * 1e3, 2), "unit": "ms", "cores": _host_threads()[0], "kind": "port",
+               "sample": f"one partition of the same {n} atoms: the C oracle's Morton keys (OpenMP), numpy's "
+                         "stable argsort (one thread) and the oracle's labels"}
+    print(json.dumps({
+        "metric": f"SFC partition of {n} atoms (Morton keys, stable order, W={W} labels), ms per partition",
+        "value": round(ms, 4), "unit": "ms", "n_gpus": 1, "steps": args.steps, "warmup": args.warmup,
+        "ms_per_step": round(ms, 4), "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 positions, int64 keys", "data": "synthetic (seeded numpy uniform box)",
+        "config": {"workload": f"SFC partition, {args.config} N={n}, W={W}"},
+        "keys_ms": round(keys_ms, 4), "order_ms": round(order_ms, 4), "labels_ms": round(labels_ms, 4),
+        "weighted_labels_ms": round(wlabels_ms, 4),
+        "roofline": {"bound": "hbm", "achieved": round(ach, 1), "peak": HBM_PEAK_GBS, "unit": "GB/s",
+                     "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
+                     "kernel": "dg_sfc_order (all its kernels)", "algorithmic_bytes": kbytes,
+                     "bytes_per_unit": "16 per key"},
         "cpu_baseline": cpu}), flush=True)
 
 
