@@ -24,6 +24,7 @@ constexpr int kBlock = 256;      // threads per search workgroup (4 x wave64)
 constexpr int kSortChunks = DG_SORT_CHUNKS;  // atom chunks of the tile-level counting sort
 constexpr int kSortTilesMax = 36000;  // tiles it handles (an LDS histogram of ints, < 144 KiB)
 constexpr int kMaxRegion = 768;  // region bins staged per tile
+constexpr int kMaxReach = 1 << 16;  // bins a cutoff may reach per axis (far past kMaxRegion)
 constexpr int kTileTargets = 235; // aim: targets per tile <= this (a 256-lane workgroup)
 constexpr int kTileMax = 6;
 constexpr int64_t kFewTiles = 1024;       // tiles below one round of workgroups on 256 CUs
@@ -107,8 +108,10 @@ inline void plan_grid(Plan& p)
     }
     for (int d = 0; d < 3; d++) {
         p.nb[d] = (int)nbd[d];
-        p.P[d] = (int)ceil(p.cf[d] * p.nb[d] * (1.0 + 1e-9) + 1e-12);
-        if (p.P[d] < 1) p.P[d] = 1;
+        // bins the cutoff reaches, capped (in double, before the conversion) far beyond any
+        // region the tiled search takes: a cutoff of many cell widths goes all-pairs
+        const double reach = ceil(p.cf[d] * p.nb[d] * (1.0 + 1e-9) + 1e-12);
+        p.P[d] = (int)std::min(std::max(reach, 1.0), (double)kMaxReach);
     }
     // Tile: as many bins as keep the expected targets of a tile within one 256-lane
     // workgroup, with a region of at most kMaxRegion bins; prefer compact tiles.
@@ -163,7 +166,7 @@ inline void plan_grid(Plan& p)
         while ((1 << b) < p.ntl[d]) b++;
         p.mb[d] = b;
     }
-    p.nregion = p.R[0] * p.R[1] * p.R[2];
+    p.nregion = p.brute ? 0 : (int)region();  // (the all-pairs path has no region table)
     p.tb = p.T[0] * p.T[1] * p.T[2];
     p.ntiles = (int64_t)p.ntl[0] * p.ntl[1] * p.ntl[2];
     p.nbins = p.ntiles * p.tb;
