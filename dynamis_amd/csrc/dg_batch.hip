@@ -3,8 +3,8 @@
 // radius_graph_pbc_cuda (radius_graph_pbc_cuda.py:64-110) builds a batch image by image:
 // one full build, and one host synchronisation, per structure.  For the small structures
 // of a training batch (tens to a few hundred atoms each) every one of those builds is
-// launch-bound.  Here one thread per atom of the whole batch tests every atom of its own
-// structure over the periodic images of that structure's cell, with the canonical fp64
+// launch-bound.  Here one wave per atom of the whole batch tests every atom of its own
+// structure (64 lanes at a time) over the periodic images of that structure's cell, with the canonical fp64
 // predicate and shift convention of the single-structure build (an edge's shift is its
 // image plus the floor difference of its two atoms, radius_graph_kernels.cu:282-303): a
 // count pass, one scan over the batch, a write pass.  Edges come grouped by target, the
@@ -177,58 +177,82 @@ __device__ __forceinline__ int64_t image_of(const int64_t* off, int64_t B, int64
     return lo;
 }
 
+// One wave per atom t of the batch (the target): its lanes take the sources of t's structure
+// 64 at a time, each lane every periodic image of its source that can hold an edge.  The
+// count pass adds up the lanes' edges; the write pass places each lane's edges after those
+// of the lanes before it (a wave scan per group of 64 sources), so edges come in source
+// order and, for one source, in image order (s0, s1, s2 ascending, nested).
 template <bool WRITE>
 __global__ __launch_bounds__(256) void batch_kernel(Args a)
 {
-    const int64_t t = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
+    const int64_t t = ((int64_t)blockIdx.x * blockDim.x + threadIdx.x) >> 6;  // one wave per target
+    const int lane = threadIdx.x & 63;
     if (t >= a.N) return;
     const Image& m = a.img[image_of(a.off, a.B, t)];
     double pt[3];
     load_pos(a.pos, a.f64, t, pt);
-    int found = 0;
-    const bool good = m.ok && isfinite(pt[0]) && isfinite(pt[1]) && isfinite(pt[2]);
-    if (!good && !WRITE && !(isfinite(pt[0]) && isfinite(pt[1]) && isfinite(pt[2])))
+    const bool finite_t = isfinite(pt[0]) && isfinite(pt[1]) && isfinite(pt[2]);
+    const bool good = m.ok && finite_t;
+    if (!WRITE && !finite_t && lane == 0)
         atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusNonFinite);
     int64_t o = 0;
     if (WRITE) {
         o = a.offs[t];
         if (a.offs[t + 1] > a.capacity) {
-            atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
+            if (lane == 0) atomicOr((unsigned long long*)&a.totals[1], (unsigned long long)kStatusCapacity);
             return;
         }
     }
+    int found = 0;  // this lane's edges (count pass); edges of the wave so far (write pass)
     if (good) {
         double frt[3];
         for (int d = 0; d < 3; ++d) frt[d] = canon_frac(pt[0], pt[1], pt[2], m.Cinv, d);
         // (clamped to the batch: atom counts that do not add up are flagged by setup_kernel)
         const int64_t jb = max(m.off, (int64_t)0), je = min(m.off + m.n, a.N);
-        for (int64_t j = jb; j < je; ++j) {
+        for (int64_t j0 = jb; j0 < je; j0 += 64) {
+            const int64_t j = j0 + lane;
             double ps[3];
-            load_pos(a.pos, a.f64, j, ps);
-            if (!(isfinite(ps[0]) && isfinite(ps[1]) && isfinite(ps[2]))) continue;
-            int lo[3], hi[3];
-            shift_range(a.pbc, m.cf, frt, ps, m.Cinv, lo, hi);
-            for (int s0 = lo[0]; s0 <= hi[0]; ++s0)
-                for (int s1 = lo[1]; s1 <= hi[1]; ++s1)
-                    for (int s2 = lo[2]; s2 <= hi[2]; ++s2) {
-                        double v[3];
-                        const double d2 = canon_d2(ps, pt, s0, s1, s2, m.C, v);
-                        if (!(d2 > kSelfThr && d2 <= a.r2)) continue;
-                        if (WRITE) {
-                            const int64_t e = o + found;
-                            a.out_src[e] = j;
-                            a.out_dst[e] = t;
-                            a.out_shift[3 * e] = (float)s0;
-                            a.out_shift[3 * e + 1] = (float)s1;
-                            a.out_shift[3 * e + 2] = (float)s2;
+            int lo[3] = {0, 0, 0}, hi[3] = {-1, -1, -1};  // (no images for an idle lane)
+            if (j < je) {
+                load_pos(a.pos, a.f64, j, ps);
+                if (isfinite(ps[0]) && isfinite(ps[1]) && isfinite(ps[2]))
+                    shift_range(a.pbc, m.cf, frt, ps, m.Cinv, lo, hi);
+            }
+            auto each_edge = [&](auto&& f) {
+                for (int s0 = lo[0]; s0 <= hi[0]; ++s0)
+                    for (int s1 = lo[1]; s1 <= hi[1]; ++s1)
+                        for (int s2 = lo[2]; s2 <= hi[2]; ++s2) {
+                            double v[3];
+                            const double d2 = canon_d2(ps, pt, s0, s1, s2, m.C, v);
+                            if (d2 > kSelfThr && d2 <= a.r2) f(s0, s1, s2);
                         }
-                        ++found;
-                    }
+            };
+            int mine = 0;
+            each_edge([&](int, int, int) { ++mine; });
+            if (!WRITE) {
+                found += mine;
+            } else {
+                const int incl = wave_incl_scan<int>(mine);
+                int64_t e = o + found + (incl - mine);
+                each_edge([&](int s0, int s1, int s2) {
+                    a.out_src[e] = j;
+                    a.out_dst[e] = t;
+                    a.out_shift[3 * e] = (float)s0;
+                    a.out_shift[3 * e + 1] = (float)s1;
+                    a.out_shift[3 * e + 2] = (float)s2;
+                    ++e;
+                });
+                found += __shfl(incl, 63, 64);
+            }
         }
     }
     if (!WRITE) {
-        a.cnt[t] = found;
-        if (a.counts_user) a.counts_user[t] = found;
+        // the wave's total
+        for (int sh = 32; sh > 0; sh >>= 1) found += __shfl_xor(found, sh, 64);
+        if (lane == 0) {
+            a.cnt[t] = found;
+            if (a.counts_user) a.counts_user[t] = found;
+        }
     }
 }
 
@@ -308,7 +332,7 @@ dg_status dg_batch_count(const dg_batch_desc* desc, const void* pos, const int64
                        (const int64_t*)off, (int)a.pbc[0], (int)a.pbc[1], (int)a.pbc[2], desc->radius,
                        (Image*)(w + L.o_img), a.totals);
     if (desc->n_atoms > 0) {
-        hipLaunchKernelGGL(batch_kernel<false>, dim3(nblk(desc->n_atoms)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(batch_kernel<false>, dim3(nblk(64 * desc->n_atoms)), dim3(256), 0, s, a);
         excl_scan<int, int64_t>(a.cnt, desc->n_atoms, (int64_t*)(w + L.o_offs), (int64_t*)(w + L.o_part), s,
                                 a.totals);
     } else {
@@ -353,7 +377,7 @@ dg_status dg_batch_write(const dg_batch_desc* desc, const void* pos, void* ws, s
     a.capacity = capacity;
     if (desc->n_atoms > 0 && capacity > 0) {
         if (!edge_src || !edge_dst || !cell_shift) return fail(DG_ERR_INVALID, "edge outputs are NULL");
-        hipLaunchKernelGGL(batch_kernel<true>, dim3(nblk(desc->n_atoms)), dim3(256), 0, s, a);
+        hipLaunchKernelGGL(batch_kernel<true>, dim3(nblk(64 * desc->n_atoms)), dim3(256), 0, s, a);
     }
     if (edges_per_image) {
         char* w = (char*)ws;

@@ -13,20 +13,22 @@ from . import dynamis_state_impl as _impl
 # the periodic images its cell needs) when that is expected to be faster than building the
 # structures one by one with the cell-list build, as the reference loop does.  Measured on
 # one MI355X (uniform structures at 0.08 atoms/A^3, r = 6 A): the loop costs about 0.19 ms
-# per structure; the batched build about 0.35 ms plus 1.2 us per atom of its largest
-# structure (one thread per atom sweeps its structure's atoms and images), e.g. 128
-# structures of up to 250 atoms in 0.71 ms against 23.5 ms.  Structures above
-# BATCH_MAX_ATOMS always go through the loop.
-BATCH_MAX_ATOMS = 2048
+# per structure; the batched build about 0.22 ms plus 16 ps per atom pair within the
+# structures (one wave per atom sweeps its structure's atoms and images), e.g. 128
+# structures of up to 250 atoms in 0.35 ms against 23.4 ms, 512 of up to 500 in 1.5 ms
+# against 92 ms.  A single structure, and structures above BATCH_MAX_ATOMS, always go
+# through the cell-list build.
+BATCH_MAX_ATOMS = 8192
 _LOOP_MS_PER_STRUCTURE = 0.19
-_BATCH_MS = 0.35
-_BATCH_MS_PER_ATOM = 0.0012
+_BATCH_MS = 0.22
+_BATCH_MS_PER_PAIR = 1.6e-8
 
 
 def _batch_in_one_pass(natoms) -> bool:
     if len(natoms) < 2 or max(natoms) > BATCH_MAX_ATOMS:
         return False
-    return _BATCH_MS + _BATCH_MS_PER_ATOM * max(natoms) < _LOOP_MS_PER_STRUCTURE * len(natoms)
+    pairs = sum(n * n for n in natoms)
+    return _BATCH_MS + _BATCH_MS_PER_PAIR * pairs < _LOOP_MS_PER_STRUCTURE * len(natoms)
 
 
 def radius_graph_pbc_cuda(data, radius: float, max_num_neighbors_threshold: int,
