@@ -58,6 +58,7 @@ def _validate(pos, cell, pbc, radius, max_num_neighbors=None, target_indices=Non
                f"max_num_neighbors must be non-negative, got {int(max_num_neighbors)}")
     if target_indices is not None:
         ti = target_indices
+        _check(isinstance(ti, torch.Tensor), f"target_indices must be a tensor, got {type(ti).__name__}")
         _check(ti.device == pos.device, "target_indices must be on the same device as pos")
         _check(ti.dim() == 1, f"target_indices must be 1-D, got shape {list(ti.shape)}")
         _check(ti.dtype == torch.int64, f"target_indices must be int64, got {ti.dtype}")
@@ -155,6 +156,10 @@ def build_batch(pos, cells, natoms, pbc, radius, max_num_neighbors=0):
     pos, _, pbc, _ = _validate(pos, torch.eye(3), pbc, radius, max_num_neighbors)
     lib = L.lib()
     dev = pos.device
+    natoms = torch.as_tensor(natoms)
+    _check(natoms.dim() == 1, f"natoms must have shape [B], got {_shape(natoms)}")
+    _check(not natoms.is_floating_point() and not natoms.is_complex() and natoms.dtype != torch.bool,
+           f"natoms must be integers, got {natoms.dtype}")
     B = int(natoms.numel())
     _check(B >= 1, "the batch is empty")
     cells = torch.as_tensor(cells)

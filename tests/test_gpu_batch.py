@@ -118,6 +118,10 @@ def test_batch_errors(cuda):
     thin[2] = np.diag([10.0, 10.0, 1e-7])  # 1.2e8 periodic images per pair on one axis
     with pytest.raises(RuntimeError, match="too thin"):
         impl.build_batch(p, torch.from_numpy(thin), torch.from_numpy(natoms), torch.tensor([True] * 3), r)
-    # a good batch right after
+    with pytest.raises(RuntimeError, match="integers"):
+        impl.build_batch(p, torch.from_numpy(cells), torch.from_numpy(natoms).double(), torch.tensor(pbc), r)
+    # a good batch right after (atom counts as a Python list)
+    ei2, co2, nn2 = impl.build_batch(p, torch.from_numpy(cells), [int(x) for x in natoms], torch.tensor(pbc), r)
     ei, co, nn = impl.build_batch(p, torch.from_numpy(cells), torch.from_numpy(natoms), torch.tensor(pbc), r)
     assert int(nn.sum()) == ei.shape[1]
+    assert torch.equal(ei, ei2) and torch.equal(co, co2) and torch.equal(nn, nn2)
