@@ -47,13 +47,14 @@ def main():
     ap.add_argument("--vectors", action="store_true",
                     help="graph path: also emit the edge vectors (fp32 [E,3]) and distances "
                          "(fp32 [E]) in the write stage: 44 bytes per edge instead of 28")
-    ap.add_argument("--path", default="graph", choices=["graph", "halo", "filter", "batch", "sfc"],
+    ap.add_argument("--path", default="graph", choices=["graph", "halo", "filter", "batch", "sfc", "dist"],
                     help="graph: the headline full rebuild; halo: extract_halo_info of one rank "
                          "of an 8-way SFC partition of the same box (edges at r + 0.5); filter: "
                          "filter_edges_to_radius of the box's edges at r + 0.5 down to r; batch: "
                          "radius_graph_pbc_cuda on batches of small structures, batched against "
                          "the per-structure loop; sfc: the SFC partition of the box's atoms "
-                         "(keys, stable order, labels)")
+                         "(keys, stable order, labels); dist: DistGraphBuilder on one rank "
+                         "(refresh and steady steps)")
     ap.add_argument("--copy-calibration", action="store_true",
                     help="run only a plain 1 GiB device-to-device copy (5 times): the reference "
                          "kernel for scaling rocprofv3 FETCH_SIZE / WRITE_SIZE to bytes")
@@ -88,6 +89,8 @@ def main():
         return bench_batch(args)
     if args.path == "sfc":
         return bench_sfc(args)
+    if args.path == "dist":
+        return bench_dist(args)
 
     box = {"C1": configs.fcc, "C2": configs.c2, "C3": configs.c3, "C4": configs.c4,
            "C4-500k": lambda: configs.c4(scale=1.3934), "C5": configs.c5}[args.config]()
@@ -581,6 +584,55 @@ def bench_halo(args):
                      "frac": round(ach / HBM_PEAK_GBS, 4), "traffic": None,
                      "kernel": "dg_halo_count + dg_halo_write (all kernels)", "algorithmic_bytes": nbytes},
         "cpu_baseline": cpu}), flush=True)
+
+
+def bench_dist(args):
+    """DistGraphBuilder (row f4) on one rank (no communication) over the config's box, with
+    the positions moving by Gaussian sigma per coordinate per step (the drift watchdog never
+    trips): the refresh step (mode A: degrees, SFC partition, build at r + skin, halo plan,
+    filter to r) and the steady steps (mode B: the local build from the cached partition).
+    One step = one DistGraphBuilder.build; host clock around synchronised steps."""
+    import numpy as np
+    import torch
+
+    from dynamis_amd import configs
+    from dynamis_amd.dynamis_state import dynamis_state_impl as impl
+    from dynamis_amd.dynamis_state.dist_graph_builder import BuildMode, DistGraphBuilder
+
+    box = {"C2": configs.c2, "C3": configs.c3}[args.config]()
+    dev = torch.device("cuda:0")
+    torch.cuda.set_device(dev)
+    pos = torch.from_numpy(np.ascontiguousarray(box.pos, dtype=np.float32)).to(dev)
+    cell = torch.from_numpy(np.asarray(box.cell, np.float32))
+    env = impl.DistEnvironment()
+    gen = torch.Generator(device=dev).manual_seed(11)
+    noise = [torch.randn(pos.shape, device=dev, generator=gen) * args.sigma for _ in range(8)]
+    b = DistGraphBuilder(cell, torch.tensor(list(box.pbc)), box.radius, 0.5, env,
+                         refresh_interval=10 ** 9)
+    refresh, steady = [], []
+    for k in range(args.warmup + args.steps + 1):
+        if k == 0 or k == args.warmup:
+            b.reset()  # this step refreshes
+        torch.cuda.synchronize()
+        t = time.perf_counter()
+        res = b.build(pos)
+        torch.cuda.synchronize()
+        dt = (time.perf_counter() - t) * 1e3
+        if k >= args.warmup:
+            (refresh if res.mode == BuildMode.REFRESH else steady).append(dt)
+        pos.add_(noise[k % len(noise)])
+    E = int(res.edges_outer.shape[1])
+    ms = float(np.median(steady))
+    print(json.dumps({
+        "metric": "DistGraphBuilder step (one rank), ms", "value": round(ms, 4), "unit": "ms",
+        "n_gpus": 1, "steps": len(steady), "warmup": args.warmup, "ms_per_step": round(ms, 4),
+        "higher_is_better": False, "scaling": "weak", "vs_baseline": None,
+        "dtype": "fp32 positions, fp64 predicate, int64 edges",
+        "data": f"synthetic (seeded numpy uniform box), moved by sigma={args.sigma} A per coordinate per step",
+        "config": {"workload": f"DistGraphBuilder W=1, {args.config} N={pos.shape[0]}, r={box.radius}, skin=0.5",
+                   "edges": E},
+        "refresh_ms": round(float(np.median(refresh)), 4), "steady_ms": round(ms, 4),
+        "roofline": None, "cpu_baseline": None}), flush=True)
 
 
 def bench_sfc(args):

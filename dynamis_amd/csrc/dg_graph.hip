@@ -644,6 +644,7 @@ struct SearchArgs {
     int vout_f64;
     int64_t capacity;
     int64_t* totals;
+    const int64_t* out_ids;  // written for atom i: out_ids[i] (null: i); positions use i
     // Per-target neighbour slots (K region indices each), or null.  Entries go in groups
     // of 8 (16 bytes), group-major: group g of target j at slot + 8 * (g * nslot + j), so
     // the groups that neighbouring targets fill at about the same time share cache lines.
@@ -798,11 +799,17 @@ __device__ __forceinline__ bool exact_edge(const SearchArgs& a, int src, int tgt
 }
 
 // One edge: edge_index columns, integer cell shift, optional canonical vector / distance.
+__device__ __forceinline__ int out_id(const SearchArgs& a, int i)
+{
+    return a.out_ids ? (int)a.out_ids[i] : i;
+}
+
+// src, dst: atom indices (of pos); the ids written go through a.out_ids.
 __device__ __forceinline__ void emit_edge(const SearchArgs& a, int64_t o, int src, int dst, int S0,
                                           int S1, int S2)
 {
-    a.out_src[o] = src;
-    a.out_dst[o] = dst;
+    a.out_src[o] = out_id(a, src);
+    a.out_dst[o] = out_id(a, dst);
     *(float3*)(a.out_shift + 3 * o) = make_float3((float)S0, (float)S1, (float)S2);
     if (a.out_vec || a.out_dist) {
         double ps[3], pt[3], vv[3];
@@ -889,8 +896,9 @@ typedef int v4i __attribute__((ext_vector_type(4)));
 // Stages the tile's region into ExpandStage::e as (source atom id, packed bin shift -
 // floor) pairs -- 8 bytes per entry -- bin by bin from the cell list.  The caller has
 // finished every use of the float4 view of the region buffer.
-// GIDX: an entry names its source by cell-list index instead of atom id.
-template <int CAP, bool GIDX = false>
+// GIDX: an entry names its source by cell-list index instead of atom id; MAP: by the id
+// written for it (a.out_ids), for expansions that need no positions.
+template <int CAP, bool GIDX = false, bool MAP = false>
 __device__ __forceinline__ void stage_pairs(const SearchArgs& a, typename ExpandLdsOf<CAP>::type& sh,
                                             const int* g0)
 {
@@ -915,7 +923,8 @@ __device__ __forceinline__ void stage_pairs(const SearchArgs& a, typename Expand
                 for (int i = 0; i < rcnt[h]; ++i) {
                     const int gidx = rst[h] + i;
                     const uint32_t fl = a.sflr[gidx];
-                    X.e[ex + i] = make_int2(GIDX ? gidx : a.sid[gidx], (int)pack3(sb[0] - unpack3(fl, 0),
+                    const int src = GIDX ? gidx : (MAP ? out_id(a, a.sid[gidx]) : a.sid[gidx]);
+                    X.e[ex + i] = make_int2(src, (int)pack3(sb[0] - unpack3(fl, 0),
                                                                      sb[1] - unpack3(fl, 1),
                                                                      sb[2] - unpack3(fl, 2)));
                 }
@@ -960,7 +969,9 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
         if (active) {
             const int sidx = listed_targets(a) ? a.tsidx[j] : j;
             B.off[threadIdx.x] = ex;
-            B.tid[threadIdx.x] = a.sid[sidx];
+            // (the plain path writes B.tid as it is: the id to write; with vectors it also
+            // indexes the target's position, and the id is mapped when staged)
+            B.tid[threadIdx.x] = (plain && !kVec) ? out_id(a, a.sid[sidx]) : a.sid[sidx];
             B.tf[threadIdx.x] = a.sflr[sidx];
         }
         if (threadIdx.x == 0) B.off[nbatch] = btot;
@@ -1125,7 +1136,14 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
                 for (int u = 0; u < ILP; ++u) {
                     const int i = 64 * u + lane;
                     if (i < n) {
-                        st_s[i] = rs[u]; st_d[i] = rd[u]; st_S[i] = rS[u];
+                        if constexpr (kVec) {
+                            st_s[i] = out_id(a, rs[u]);
+                            st_d[i] = out_id(a, rd[u]);
+                        } else {
+                            st_s[i] = rs[u];
+                            st_d[i] = rd[u];
+                        }
+                        st_S[i] = rS[u];
                         if constexpr (kVec) {
                             st_v[3 * i] = rv[u][0];
                             st_v[3 * i + 1] = rv[u][1];
@@ -1704,13 +1722,18 @@ __device__ __forceinline__ void expand_one(const SearchArgs& a, typename ExpandL
     const int lin = a.tile_of_rank[rank];
     const int g0[3] = {(lin % a.ntl[0]) * a.T[0], ((lin / a.ntl[0]) % a.ntl[1]) * a.T[1],
                        (lin / (a.ntl[0] * a.ntl[1])) * a.T[2]};
-    stage_pairs<CAP, !std::is_void<VT>::value>(a, sh, g0);
-    if constexpr (!std::is_void<VT>::value)
+    // region entries: cell-list indices (grouped vectors), the ids to write (the plain
+    // path, which needs no positions), or atom indices (the per-lane path)
+    if constexpr (!std::is_void<VT>::value) {
+        stage_pairs<CAP, true>(a, sh, g0);
         expand_tile<true, CAP, VT, kVecIlp>(a, sh, tbeg, ntg, ebase, vsp);
-    else if (!a.out_vec && !a.out_dist)
+    } else if (!a.out_vec && !a.out_dist) {
+        stage_pairs<CAP, false, true>(a, sh, g0);
         expand_tile<true, CAP>(a, sh, tbeg, ntg, ebase);
-    else
+    } else {
+        stage_pairs<CAP>(a, sh, g0);
         expand_tile<false, CAP>(a, sh, tbeg, ntg, ebase);
+    }
 }
 
 // MODE 0 (count) and MODE 1 (fix-up write): one tile per workgroup.  The fix-up also
@@ -1809,6 +1832,7 @@ struct BruteArgs {
     int vout_f64;
     int64_t capacity;
     int64_t* totals;
+    const int64_t* out_ids;  // written for atom i: out_ids[i] (null: i)
 };
 
 template <bool WRITE>
@@ -1857,8 +1881,8 @@ __global__ void brute_kernel(BruteArgs a)
                     if (!(d2 > kSelfThr && d2 <= a.r2)) continue;
                     if (WRITE) {
                         int64_t e = o + found;
-                        a.out_src[e] = j;
-                        a.out_dst[e] = tg;
+                        a.out_src[e] = a.out_ids ? a.out_ids[j] : j;
+                        a.out_dst[e] = a.out_ids ? a.out_ids[tg] : tg;
                         a.out_shift[3 * e] = (float)s0;
                         a.out_shift[3 * e + 1] = (float)s1;
                         a.out_shift[3 * e + 2] = (float)s2;
@@ -2342,10 +2366,10 @@ dg_status dg_graph_read_totals(const dg_graph_desc* desc, const void* ws, int64_
     return DG_OK;
 }
 
-dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
-                         void* ws, size_t ws_bytes, int64_t capacity, int64_t* edge_src,
-                         int64_t* edge_dst, float* cell_shift, void* edge_vec, void* edge_dist,
-                         int32_t vec_dtype, hipStream_t s)
+dg_status dg_graph_write_ids(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                             void* ws, size_t ws_bytes, int64_t capacity, const int64_t* out_ids,
+                             int64_t* edge_src, int64_t* edge_dst, float* cell_shift, void* edge_vec,
+                             void* edge_dist, int32_t vec_dtype, hipStream_t s)
 {
     Plan p;
     dg_status st = make_plan(desc, p);
@@ -2361,6 +2385,7 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
         b.out_src = edge_src; b.out_dst = edge_dst; b.out_shift = cell_shift;
         b.out_vec = edge_vec; b.out_dist = edge_dist; b.vout_f64 = vec_dtype == DG_F64;
         b.capacity = capacity;
+        b.out_ids = out_ids;
         hipLaunchKernelGGL(brute_kernel<true>, dim3(nblocks(p.nt, 64)), dim3(64), 0, s, b);
         return check_launch("dg_graph_write(brute)");
     }
@@ -2368,6 +2393,7 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
     a.out_src = edge_src; a.out_dst = edge_dst; a.out_shift = cell_shift;
     a.out_vec = edge_vec; a.out_dist = edge_dist; a.vout_f64 = vec_dtype == DG_F64;
     a.capacity = capacity;
+    a.out_ids = out_ids;
     StageTimer clk(s);
     clk.mark("start");
     // vectors / distances go out in 16-byte groups from bases aligned to 16 bytes, else
@@ -2391,6 +2417,15 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
     st = check_launch("dg_graph_write");
     clk.report("dg_graph_write", p, capacity);
     return st;
+}
+
+dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                         void* ws, size_t ws_bytes, int64_t capacity, int64_t* edge_src,
+                         int64_t* edge_dst, float* cell_shift, void* edge_vec, void* edge_dist,
+                         int32_t vec_dtype, hipStream_t s)
+{
+    return dg_graph_write_ids(desc, pos, target_idx, ws, ws_bytes, capacity, nullptr, edge_src, edge_dst,
+                              cell_shift, edge_vec, edge_dist, vec_dtype, s);
 }
 
 dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,

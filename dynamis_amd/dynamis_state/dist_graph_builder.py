@@ -227,13 +227,12 @@ class DistGraphBuilder:
         ids = torch.cat([self._my_outer_atoms, self._halo_recv_global_ids])
         local_pos = pos_w.index_select(0, ids).contiguous()
         targets = torch.arange(self._my_outer_atoms.numel(), dtype=torch.int64, device=dev)
-        e_loc, shifts, _, _ = _impl.radius_graph_pbc_ex(
-            local_pos, cell, pbc, self.cutoff, self.max_num_neighbors, self.enforce_max_strictly,
-            targets)
-        if e_loc.numel() == 0:
-            edges = torch.empty(2, 0, dtype=torch.int64, device=dev)
-        else:
-            edges = ids[e_loc.reshape(-1)].reshape(2, -1)
+        # the build writes the global ids itself (out_ids): the reference's remap of the local
+        # edges (dist_graph_builder.py:469-474) fused into the write stage
+        local_pos, cell_v, pbc_v, targets = _impl._validate(local_pos, cell, pbc, self.cutoff,
+                                                            self.max_num_neighbors, targets)
+        edges, shifts, _, _ = _impl.build_graph(local_pos, cell_v, pbc_v, _impl._r32(self.cutoff), targets,
+                                                out_ids=ids)
         self._steps_since_refresh += 1
         return DistBuildGraphResult(edges, shifts, self._pid_outer, self._my_outer_atoms,
                                     self._halo_info, self._interior_mask, self._full_degrees,

@@ -92,8 +92,12 @@ def _empty(device, n_target):
 
 
 def build_graph(pos, cell, pbc, radius, target_indices=None, counts_only=False,
-                return_vectors=False, vector_dtype=None):
+                return_vectors=False, vector_dtype=None, out_ids=None):
     """Core build shared by every entry point (validated inputs).
+
+    out_ids (int64 [N] on the device, or None): the ids written into edge_index for the
+    atoms (atom i is written as out_ids[i]); DistGraphBuilder's steady step passes the
+    global ids of its local atoms, which saves remapping the edges afterwards.
 
     Returns (edge_index [2,E] int64, cell_shifts [E,3] float32, num_neighbors_image [1]
     int64, neighbor_counts [N_target] int32[, edge_vec [E,3], edge_dist [E]]).
@@ -132,8 +136,8 @@ def build_graph(pos, cell, pbc, radius, target_indices=None, counts_only=False,
             dist = torch.empty(E, dtype=vdt, device=dev)
         if E > 0:
             src_ptr = edge_index.data_ptr()
-            L.check(lib.dg_graph_write(
-                d, L.ptr(pos), L.ptr(target_indices), L.ptr(ws), wsb, E,
+            L.check(lib.dg_graph_write_ids(
+                d, L.ptr(pos), L.ptr(target_indices), L.ptr(ws), wsb, E, L.ptr(out_ids),
                 L.ctypes.c_void_p(src_ptr), L.ctypes.c_void_p(src_ptr + 8 * E), L.ptr(shifts),
                 L.ptr(vec), L.ptr(dist), L.DG_F64 if vdt == torch.float64 else L.DG_F32, s),
                 "radius_graph_pbc")

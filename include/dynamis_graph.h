@@ -105,6 +105,17 @@ dg_status dg_graph_write(const dg_graph_desc* desc, const void* pos, const int64
                          int64_t* edge_src, int64_t* edge_dst, float* cell_shift, void* edge_vec,
                          void* edge_dist, int32_t vec_dtype, hipStream_t stream);
 
+/* dg_graph_write with the ids written for the atoms mapped: edge_src / edge_dst receive
+ * out_ids[i] for atom i (device int64 [n_atoms], values in [0, 2^31); NULL: i itself), while
+ * positions are still read as pos[i].  No counterpart in the reference: it fuses the remap
+ * that DistGraphBuilder's steady step applies to a local build's edges
+ * (dist_graph_builder.py:469-474, the index_select of the local edges) into the write stage. */
+dg_status dg_graph_write_ids(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                             void* workspace, size_t workspace_bytes, int64_t capacity,
+                             const int64_t* out_ids, int64_t* edge_src, int64_t* edge_dst,
+                             float* cell_shift, void* edge_vec, void* edge_dist, int32_t vec_dtype,
+                             hipStream_t stream);
+
 /* One-call build into caller-preallocated outputs of `capacity` edges:
  * dg_graph_count then dg_graph_write, back to back on the stream with no host round trip
  * (the write pass reads the count pass's per-tile offsets on the device).  Same outputs,

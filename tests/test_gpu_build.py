@@ -129,3 +129,64 @@ def test_vectors_grouped_equal_per_lane(cuda, case):
         # and the vectors are the edges' own (|v| = dist, |v| <= r)
         assert torch.allclose(vec1[:E].double().norm(dim=1), dist1[:E].double(), rtol=1e-6, atol=0)
         assert float(dist1[:E].max()) <= float(np.float32(r)) * (1 + 1e-6)
+
+
+def _write(pos, cell, pbc, r, targets, cap, out_ids, vdt=None, vec_offset=0):
+    lib = L.lib()
+    d = impl._desc(pos, cell, pbc, impl._r32(r), targets)
+    dev = pos.device
+    wsb = lib.dg_graph_workspace_size(d)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
+    nt = pos.shape[0] if targets is None else targets.shape[0]
+    cnt = torch.empty(nt, dtype=torch.int32, device=dev)
+    s = L.stream_of(dev)
+    L.check(lib.dg_graph_count(d, L.ptr(pos), L.ptr(targets), L.ptr(ws), wsb, L.ptr(cnt), s), "count")
+    ei = torch.full((2, cap), -1, dtype=torch.int64, device=dev)
+    sh = torch.full((cap, 3), -1.0, dtype=torch.float32, device=dev)
+    vec = dist = None
+    if vdt is not None:
+        vec = torch.empty(3 * cap + vec_offset, dtype=vdt, device=dev)[vec_offset:].view(cap, 3)
+        dist = torch.empty(cap + vec_offset, dtype=vdt, device=dev)[vec_offset:]
+    L.check(lib.dg_graph_write_ids(d, L.ptr(pos), L.ptr(targets), L.ptr(ws), wsb, cap, L.ptr(out_ids),
+                                   L.ctypes.c_void_p(ei.data_ptr()), L.ctypes.c_void_p(ei.data_ptr() + 8 * cap),
+                                   L.ptr(sh), L.ptr(vec), L.ptr(dist),
+                                   L.DG_F64 if vdt == torch.float64 else L.DG_F32, s), "write_ids")
+    E, fl = L._i64(0), L._i64(0)
+    L.check(lib.dg_graph_read_totals(d, L.ptr(ws), E, fl, s), "totals")
+    return int(E.value), ei, sh, vec, dist
+
+
+def _ids_cases():
+    out = list(_cases())
+    rng = np.random.default_rng(17)
+    small = np.eye(3) * 3.0  # the radius spans several cells: the all-pairs kernel
+    out.append(("all-pairs", (rng.uniform(0, 1, (40, 3)) @ small).astype(np.float32), small, (True, True, True),
+                7.0, None))
+    return out
+
+
+@pytest.mark.parametrize("case", _ids_cases(), ids=lambda c: c[0])
+def test_write_ids_is_the_remapped_write(cuda, case):
+    """dg_graph_write_ids (the ids written for the atoms mapped, as DistGraphBuilder's steady
+    step needs) gives the plain write's edges with src and dst replaced by out_ids[src],
+    out_ids[dst], and the same shifts, vectors and distances -- on every path: the grouped
+    expansion, the fix-up pass (dense and clumped cases), grouped and per-lane vectors, and
+    the all-pairs kernel."""
+    name, pos, cell, pbc, r, tg = case
+    p = torch.from_numpy(np.ascontiguousarray(pos)).to(cuda)
+    c = torch.from_numpy(np.asarray(cell, np.float64))
+    b = torch.tensor([bool(x) for x in pbc])
+    t = None if tg is None else torch.from_numpy(np.asarray(tg, np.int64)).to(cuda)
+    n = p.shape[0]
+    ids = torch.from_numpy(np.random.default_rng(3).choice(2_000_000_000, n, replace=False)).to(cuda)
+    ei0, co0, _, _ = impl.radius_graph_pbc_ex(p, c, b, r, 0, False, t)
+    E0 = ei0.shape[1]
+    for vdt, off in ((None, 0), (torch.float32, 0), (torch.float32, 1), (torch.float64, 0)):
+        print(f"\n[case] write_ids {name} N={n} vectors={vdt} offset={off}", flush=True)
+        E1, ei1, sh1, v1, d1 = _write(p, c, b, r, t, E0 + 4, None, vdt, off)
+        E2, ei2, sh2, v2, d2 = _write(p, c, b, r, t, E0 + 4, ids, vdt, off)
+        assert E1 == E2 == E0
+        assert torch.equal(ei2[:, :E0], ids[ei1[:, :E0]])
+        assert torch.equal(sh2[:E0], sh1[:E0])
+        if vdt is not None:
+            assert torch.equal(v2[:E0], v1[:E0]) and torch.equal(d2[:E0], d1[:E0])
