@@ -84,6 +84,7 @@ def lib():
         "dg_graph_workspace_size": (_sz, [D]),
         "dg_graph_count": (_i32, [D, _p, _p, _p, _sz, _p, _p]),
         "dg_graph_read_totals": (_i32, [D, _p, ctypes.POINTER(_i64), ctypes.POINTER(_i64), _p]),
+        "dg_graph_counts": (_i32, [D, _p, _p, _p, _sz, _p, _p]),
         "dg_graph_write": (_i32, [D, _p, _p, _p, _sz, _i64, _p, _p, _p, _p, _p, _i32, _p]),
         "dg_graph_write_ids": (_i32, [D, _p, _p, _p, _sz, _i64, _p, _p, _p, _p, _p, _p, _i32, _p]),
         "dg_graph_build": (_i32, [D, _p, _p, _p, _sz, _i64, _p, _p, _p, _p, _p, _p, _i32, _p]),

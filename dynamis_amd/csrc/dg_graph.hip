@@ -1344,7 +1344,9 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
     const int nchunks = (total + kCap - 1) / kCap;
     // slots hold up to two chunks' entries (2-byte byte offsets in the region); a larger
     // region is written directly by search_kernel<1>
-    const bool slotted = nchunks <= 2 && a.slot != nullptr;
+    // (the write pass follows what the count pass recorded: a tile it flagged as chunked --
+    // a region of more than two chunks, or a count that kept no slots -- is swept again)
+    const bool slotted = nchunks <= 2 && a.slot != nullptr && !(WRITE && (a.tfix[ord] & kFixChunked));
     int loaded = -1;
 
     // packed (image shift of region bin rb - floor of cell-list entry gidx)
@@ -2290,8 +2292,10 @@ size_t dg_graph_workspace_size(const dg_graph_desc* desc)
     return p.ws_bytes;
 }
 
-dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
-                         void* ws, size_t ws_bytes, int32_t* counts_out, hipStream_t s)
+// The count stage; without slots (counts only) the sweep records no neighbour lists, and a
+// dg_graph_write that follows writes every tile from its fix-up pass instead.
+static dg_status count_stage(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                             void* ws, size_t ws_bytes, int32_t* counts_out, bool slots, hipStream_t s)
 {
     Plan p;
     dg_status st = make_plan(desc, p);
@@ -2323,6 +2327,7 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
     // 6. degrees
     SearchArgs a = search_args(p, pos, ws);
     a.counts_user = counts_out;
+    if (!slots) a.slot = nullptr;
     launch_count_kernel(a, (unsigned)p.ntiles, s);
     clk.mark("count");
     // 7. tile offsets in output order, and the total
@@ -2332,6 +2337,18 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
     st = check_launch("dg_graph_count");
     clk.report("dg_graph_count", p, -1);
     return st;
+}
+
+dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                         void* ws, size_t ws_bytes, int32_t* counts_out, hipStream_t s)
+{
+    return count_stage(desc, pos, target_idx, ws, ws_bytes, counts_out, true, s);
+}
+
+dg_status dg_graph_counts(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                          void* ws, size_t ws_bytes, int32_t* counts_out, hipStream_t s)
+{
+    return count_stage(desc, pos, target_idx, ws, ws_bytes, counts_out, false, s);
 }
 
 dg_status dg_graph_read_totals(const dg_graph_desc* desc, const void* ws, int64_t* total_edges,

@@ -120,8 +120,9 @@ def build_graph(pos, cell, pbc, radius, target_indices=None, counts_only=False,
         s = L.stream_of(dev)
         ws = torch.empty(wsb, dtype=torch.uint8, device=dev)
         counts = torch.empty(nt, dtype=torch.int32, device=dev)
-        L.check(lib.dg_graph_count(d, L.ptr(pos), L.ptr(target_indices), L.ptr(ws), wsb,
-                                   L.ptr(counts), s), "radius_graph_pbc")
+        count = lib.dg_graph_counts if counts_only else lib.dg_graph_count
+        L.check(count(d, L.ptr(pos), L.ptr(target_indices), L.ptr(ws), wsb, L.ptr(counts), s),
+                "radius_graph_pbc")
         if counts_only:
             return None, None, None, counts
         E = L._i64(0)

@@ -82,6 +82,15 @@ dg_status dg_graph_count(const dg_graph_desc* desc, const void* pos, const int64
                          void* workspace, size_t workspace_bytes, int32_t* counts_out,
                          hipStream_t stream);
 
+/* Counts only: dg_graph_count without recording the neighbour lists the write stage would
+ * expand (the sweep skips them).  Replaces radius_graph_pbc_counts_ex (radius_graph.cpp:94-127,
+ * the counts-only path of radius_graph_kernels.cu:798-808).  Same outputs; a dg_graph_write
+ * that follows on the same workspace is still correct, but writes every tile from its
+ * slower fix-up pass. */
+dg_status dg_graph_counts(const dg_graph_desc* desc, const void* pos, const int64_t* target_idx,
+                          void* workspace, size_t workspace_bytes, int32_t* counts_out,
+                          hipStream_t stream);
+
 /* Synchronous: copies {total_edges, flags} out of the workspace (waits for the stream).
  * Returns DG_ERR_RANGE if a data-dependent error flag is set. */
 dg_status dg_graph_read_totals(const dg_graph_desc* desc, const void* workspace,

@@ -190,3 +190,37 @@ def test_write_ids_is_the_remapped_write(cuda, case):
         assert torch.equal(sh2[:E0], sh1[:E0])
         if vdt is not None:
             assert torch.equal(v2[:E0], v1[:E0]) and torch.equal(d2[:E0], d1[:E0])
+
+
+@pytest.mark.parametrize("case", _cases(), ids=lambda c: c[0])
+def test_counts_only(cuda, case):
+    """dg_graph_counts (no neighbour lists recorded) gives dg_graph_count's per-target counts
+    and edge total, and a write after it (every tile then from the fix-up pass) still gives
+    the bytes of the ordinary two-stage build."""
+    name, pos, cell, pbc, r, tg = case
+    print(f"\n[case] counts only {name} N={len(pos)}", flush=True)
+    p = torch.from_numpy(np.ascontiguousarray(pos)).to(cuda)
+    c = torch.from_numpy(np.asarray(cell, np.float64))
+    b = torch.tensor([bool(x) for x in pbc])
+    t = None if tg is None else torch.from_numpy(np.asarray(tg, np.int64)).to(cuda)
+    ei, co, nn, cnt = impl.radius_graph_pbc_ex(p, c, b, r, 0, False, t)
+    cnt2 = impl.radius_graph_pbc_counts_ex(p, c, b, r, t)
+    assert torch.equal(cnt2, cnt)
+    lib = L.lib()
+    d = impl._desc(p, c, b, impl._r32(r), t)
+    wsb = lib.dg_graph_workspace_size(d)
+    ws = torch.empty(wsb, dtype=torch.uint8, device=cuda)
+    s = L.stream_of(cuda)
+    cnt3 = torch.empty_like(cnt)
+    L.check(lib.dg_graph_counts(d, L.ptr(p), L.ptr(t), L.ptr(ws), wsb, L.ptr(cnt3), s), "counts")
+    E, fl = L._i64(0), L._i64(0)
+    L.check(lib.dg_graph_read_totals(d, L.ptr(ws), E, fl, s), "totals")
+    assert int(E.value) == ei.shape[1] and torch.equal(cnt3, cnt)
+    E = ei.shape[1]
+    ei4 = torch.full((2, E), -1, dtype=torch.int64, device=cuda)
+    sh4 = torch.full((E, 3), -1.0, dtype=torch.float32, device=cuda)
+    L.check(lib.dg_graph_write(d, L.ptr(p), L.ptr(t), L.ptr(ws), wsb, E, L.ctypes.c_void_p(ei4.data_ptr()),
+                               L.ctypes.c_void_p(ei4.data_ptr() + 8 * E), L.ptr(sh4), None, None, L.DG_F32, s),
+            "write")
+    torch.cuda.synchronize()
+    assert torch.equal(ei4, ei) and torch.equal(sh4, co)
