@@ -2397,6 +2397,8 @@ dg_status dg_graph_write_ids(const dg_graph_desc* desc, const void* pos, const i
     g_last_error.clear();
     if (p.n == 0 || p.nt == 0 || capacity == 0) return DG_OK;
     if (!edge_src || !edge_dst || !cell_shift) return fail(DG_ERR_INVALID, "edge outputs are NULL");
+    if (!pos) return fail(DG_ERR_INVALID, "pos is NULL");
+    if (p.subset && !target_idx) return fail(DG_ERR_INVALID, "target_idx is NULL");
     if (p.brute) {
         BruteArgs b = brute_args(p, pos, target_idx, ws);
         b.out_src = edge_src; b.out_dst = edge_dst; b.out_shift = cell_shift;

@@ -56,3 +56,15 @@ def test_workspace_size_and_validation():
     assert st == L.DG_ERR_WORKSPACE
     assert lib.dg_filter_workspace_size(1000) > 4000
     assert lib.dg_sfc_workspace_size(1000) > 8000
+
+
+def test_write_refuses_null_inputs():
+    """dg_graph_write checks its input pointers before anything is launched (no GPU needed)."""
+    lib = L.lib()
+    d = _desc(100)
+    big = 1 << 40
+    one = ctypes.c_void_p(16)
+    st = lib.dg_graph_write(d, None, None, one, big, 10, one, one, one, None, None, L.DG_F32, None)
+    assert st == L.DG_ERR_INVALID and b"pos is NULL" in lib.dg_last_error()
+    st = lib.dg_graph_counts(d, None, None, one, big, None, None)
+    assert st == L.DG_ERR_INVALID and b"pos is NULL" in lib.dg_last_error()
