@@ -594,6 +594,7 @@ __global__ void finish_targets_kernel(int64_t nbins, int64_t n, const int* __res
 
 // ---------------------------------------------------------------- neighbour search
 struct SearchArgs {
+    int line_edges;  // the expansion's wave ranges start at output offsets that are multiples of this
     double C[9];
     double Cinv[9];
     double hC[9];  // bin step vectors: row d = C[d] / nb[d]
@@ -688,6 +689,11 @@ __device__ __forceinline__ int64_t xcd_tile_rank(int64_t b, int64_t ntiles)
 // The count pass adds the per-lane slot staging (lb) and still fits four workgroups per
 // CU; the fix-up write pass adds the per-entry shift table T.
 constexpr int kStage = 64 * kExpandIlp;  // edges one wave stages per step
+// Edges whose outputs span whole 128-byte lines from a line-aligned start: 32 edges are 256
+// bytes of int64 ids, 384 of fp32 shifts (and of fp32 vectors), 128 of fp32 distances.
+constexpr int kLineEdges = 32;
+constexpr double kAlignSlotBytes = 400e6;  // largest slot array that takes line-aligned ranges
+static_assert(kLineEdges <= 64 * kExpandIlp, "a wave's head is fetched in one step");
 // CAP: region entries staged (one LDS chunk, or two for the dense tiles of expand2)
 // STG: edges a wave stages per step (64 per unit of the expansion's ILP)
 template <int CAP, int STG = kStage>
@@ -977,7 +983,17 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
         if (threadIdx.x == 0) B.off[nbatch] = btot;
         __syncthreads();  // region entries and the batch tables visible to all waves
 
-        const int E0 = (int)(((int64_t)btot * w) / NWv), E1 = (int)(((int64_t)btot * (w + 1)) / NWv);
+        // the waves' ranges split at output offsets that are multiples of a.line_edges:
+        // with kLineEdges the 16-byte groups of every full step fill whole 128-byte lines
+        // of each output (at C3, 0.63 ms with steps at multiples of 4 edges, 0.51 aligned)
+        auto split = [&](int ww) {
+            if (ww == 0) return 0;
+            if (ww == NWv) return btot;
+            const int64_t g = ebase + ((int64_t)btot * ww) / NWv;
+            const int64_t al = (g + a.line_edges - 1) & ~(int64_t)(a.line_edges - 1);
+            return (int)min<int64_t>(al - ebase, btot);
+        };
+        const int E0 = split(w), E1 = split(w + 1);
         int tcur = 0;
         {
             int lo = 0, hi = nbatch;  // target containing E0
@@ -1084,11 +1100,12 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
         } else {
             // Groups of 4 edges that start at a multiple of 4 in the output are staged in
             // LDS and written as 16-byte stores: 2 for the 4 sources, 2 for the targets, 3
-            // for the shifts, every one 16-byte aligned.  The up-to-3 edges before the first
-            // group and after the last one are stored per lane, so no 16-byte store of this
-            // wave touches another wave's edges.  A slot left to search_kernel<1> (k >= K)
+            // for the shifts, every one 16-byte aligned.  The edges before the first line
+            // boundary (up to kLineEdges - 1, only at the start of a batch) and the up-to-3
+            // after the last group are stored per lane, so no 16-byte store of this wave
+            // touches another wave's edges.  A slot left to search_kernel<1> (k >= K)
             // receives a placeholder here and its edge there, later on the same stream.
-            const int head = min((int)((4 - (wbase & 3)) & 3), E1 - E0);
+            const int head = min((int)((a.line_edges - (wbase & (a.line_edges - 1))) & (a.line_edges - 1)), E1 - E0);
             const int A0 = E0 + head;
             const int A1 = A0 + ((E1 - A0) & ~3);
             if (head > 0) {
@@ -2086,6 +2103,10 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.slot = at<uint16_t>(ws, p.o_slot);
     a.K = p.K;
     a.nslot = nrow;
+    // Line-aligned wave ranges in the expansion pay while the slot array is small; past
+    // about 440 MB of slots they cost time instead (measured on uniform boxes: 0.5-1.5M
+    // atoms with 320-432 MB of slots, 20 % faster; 448-512 MB and C5, 4-10 % slower).
+    a.line_edges = 2.0 * (double)p.K * (double)nrow <= kAlignSlotBytes ? kLineEdges : 4;
     a.ntarg = p.nt;
     // the prefix test runs with the tile-level sort only (the per-bin fallback sorts the
     // explicit targets as listed)
