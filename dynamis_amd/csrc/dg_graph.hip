@@ -594,7 +594,7 @@ __global__ void finish_targets_kernel(int64_t nbins, int64_t n, const int* __res
 
 // ---------------------------------------------------------------- neighbour search
 struct SearchArgs {
-    int line_edges;  // the expansion's wave ranges start at output offsets that are multiples of this
+    int64_t align_max_edges;  // line-aligned wave ranges in the expansion up to this edge total
     double C[9];
     double Cinv[9];
     double hC[9];  // bin step vectors: row d = C[d] / nb[d]
@@ -692,7 +692,12 @@ constexpr int kStage = 64 * kExpandIlp;  // edges one wave stages per step
 // Edges whose outputs span whole 128-byte lines from a line-aligned start: 32 edges are 256
 // bytes of int64 ids, 384 of fp32 shifts (and of fp32 vectors), 128 of fp32 distances.
 constexpr int kLineEdges = 32;
-constexpr double kAlignSlotBytes = 400e6;  // largest slot array that takes line-aligned ranges
+// Line-aligned wave ranges pay while the slot array plus a small share of the outputs stay
+// under a budget, and cost time past it (a rule fitted to measurements on this part: at
+// C3 the write stage takes 0.545 ms aligned against 0.645 ms; with 448 MB of slots, or with
+// C3's edge vectors, aligned ranges are 4-10 % slower).
+constexpr double kAlignBudget = 564e6;      // bytes
+constexpr double kAlignOutShare = 0.065;    // of the output bytes
 static_assert(kLineEdges <= 64 * kExpandIlp, "a wave's head is fetched in one step");
 // CAP: region entries staged (one LDS chunk, or two for the dense tiles of expand2)
 // STG: edges a wave stages per step (64 per unit of the expansion's ILP)
@@ -983,14 +988,15 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
         if (threadIdx.x == 0) B.off[nbatch] = btot;
         __syncthreads();  // region entries and the batch tables visible to all waves
 
-        // the waves' ranges split at output offsets that are multiples of a.line_edges:
-        // with kLineEdges the 16-byte groups of every full step fill whole 128-byte lines
-        // of each output (at C3, 0.63 ms with steps at multiples of 4 edges, 0.51 aligned)
+        // the waves' ranges split at output offsets that are multiples of line: with
+        // kLineEdges the 16-byte groups of every full step fill whole 128-byte lines of each
+        // output (the edge total, from the count stage, decides: see kAlignBudget)
+        const int line = a.totals[0] <= a.align_max_edges ? kLineEdges : 4;
         auto split = [&](int ww) {
             if (ww == 0) return 0;
             if (ww == NWv) return btot;
             const int64_t g = ebase + ((int64_t)btot * ww) / NWv;
-            const int64_t al = (g + a.line_edges - 1) & ~(int64_t)(a.line_edges - 1);
+            const int64_t al = (g + line - 1) & ~(int64_t)(line - 1);
             return (int)min<int64_t>(al - ebase, btot);
         };
         const int E0 = split(w), E1 = split(w + 1);
@@ -1105,7 +1111,7 @@ __device__ __forceinline__ void expand_tile(const SearchArgs& a, typename Expand
             // after the last group are stored per lane, so no 16-byte store of this wave
             // touches another wave's edges.  A slot left to search_kernel<1> (k >= K)
             // receives a placeholder here and its edge there, later on the same stream.
-            const int head = min((int)((a.line_edges - (wbase & (a.line_edges - 1))) & (a.line_edges - 1)), E1 - E0);
+            const int head = min((int)((line - (wbase & (line - 1))) & (line - 1)), E1 - E0);
             const int A0 = E0 + head;
             const int A1 = A0 + ((E1 - A0) & ~3);
             if (head > 0) {
@@ -2103,10 +2109,7 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     a.slot = at<uint16_t>(ws, p.o_slot);
     a.K = p.K;
     a.nslot = nrow;
-    // Line-aligned wave ranges in the expansion pay while the slot array is small; past
-    // about 440 MB of slots they cost time instead (measured on uniform boxes: 0.5-1.5M
-    // atoms with 320-432 MB of slots, 20 % faster; 448-512 MB and C5, 4-10 % slower).
-    a.line_edges = 2.0 * (double)p.K * (double)nrow <= kAlignSlotBytes ? kLineEdges : 4;
+    a.align_max_edges = -1;  // (set by the write call, which knows the outputs)
     a.ntarg = p.nt;
     // the prefix test runs with the tile-level sort only (the per-bin fallback sorts the
     // explicit targets as listed)
@@ -2434,6 +2437,13 @@ dg_status dg_graph_write_ids(const dg_graph_desc* desc, const void* pos, const i
     a.out_vec = edge_vec; a.out_dist = edge_dist; a.vout_f64 = vec_dtype == DG_F64;
     a.capacity = capacity;
     a.out_ids = out_ids;
+    {
+        const double slot_bytes = 2.0 * (double)p.K * (double)a.nslot;
+        const double bpe = 28.0 + (edge_vec ? (vec_dtype == DG_F64 ? 24.0 : 12.0) : 0.0) +
+                           (edge_dist ? (vec_dtype == DG_F64 ? 8.0 : 4.0) : 0.0);
+        const double room = kAlignBudget - slot_bytes;
+        a.align_max_edges = room > 0 ? (int64_t)(room / (kAlignOutShare * bpe)) : -1;
+    }
     StageTimer clk(s);
     clk.mark("start");
     // vectors / distances go out in 16-byte groups from bases aligned to 16 bytes, else
