@@ -1821,7 +1821,11 @@ __global__ void cell_pos_kernel(int64_t n, const int* __restrict__ sid, const vo
 template <typename VT>
 __global__ __launch_bounds__(kBlock) void expand_kernel(SearchArgs a)
 {
-    const int64_t ord = blockIdx.x;  // output order, as search_kernel
+    // Tiles in reverse output order: the count stage wrote the slots in output order, so the
+    // last tiles' slots are the likeliest still in the memory-side cache when this kernel
+    // starts (C5 write stage 2.78 -> 2.70 ms, a uniform 1.25M-atom box 0.87 -> 0.82 ms).
+    // Each tile still writes its own output range.
+    const int64_t ord = (int64_t)gridDim.x - 1 - blockIdx.x;
     if (a.tfix[ord] & (kFixChunked | kFix2)) return;
     if constexpr (std::is_void<VT>::value) {
         __shared__ ExpandLds sh;
