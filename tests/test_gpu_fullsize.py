@@ -95,6 +95,35 @@ def test_c3_full_edge_set(cuda):
     assert E > 9e7
 
 
+def test_c3_vectors_full_size(cuda):
+    """C3 with edge vectors and distances at full size.  The write stage splits its waves'
+    output ranges at 32-edge offsets or at 4-edge ones, chosen from the edge total and the
+    outputs' width; at C3 the plain build takes the first and the build with fp32 vectors
+    the second, so equal edge lists (byte for byte, same order) check the two against each
+    other.  The vectors are pos[src] + S.cell - pos[dst] evaluated in fp64 and rounded to
+    fp32 (compared with torch's fp64 evaluation within one fp32 rounding), the distances
+    their norms."""
+    box = configs.c3()
+    _announce(f"C3 vectors full size N={len(box.pos)}")
+    p = torch.from_numpy(box.pos).to(cuda)
+    cell = torch.from_numpy(np.asarray(box.cell, np.float64))
+    pbc = torch.tensor([bool(x) for x in box.pbc])
+    ei, co, nn, cnt = impl.radius_graph_pbc_ex(p, cell, pbc, box.radius, 0, False, None)
+    ei2, co2, nn2, cnt2, vec, dist = impl.radius_graph_pbc_vectors(p, cell, pbc, box.radius,
+                                                                   vector_dtype=torch.float32)
+    assert ei.shape[1] > 9e7
+    assert torch.equal(ei2, ei) and torch.equal(co2, co) and torch.equal(cnt2, cnt)
+    c64 = cell.to(torch.float32).to(torch.float64).to(cuda)  # the cell the fp32 build uses
+    p64 = p.to(torch.float64)
+    v64 = p64[ei[0]] + co.to(torch.float64) @ c64 - p64[ei[1]]
+    # one fp32 rounding, plus 1e-12 A for fp64 evaluation-order differences near zero
+    tol = torch.finfo(torch.float32).eps * v64.abs() + 1e-12
+    assert bool(((vec.to(torch.float64) - v64).abs() <= tol).all())
+    d64 = v64.norm(dim=1)
+    del v64
+    assert bool(((dist.to(torch.float64) - d64).abs() <= torch.finfo(torch.float32).eps * d64).all())
+
+
 def test_c4_at_500k_atoms(cuda):
     """C4 at the stated 500,000 atoms: the triclinic cell scaled by 1.3934 at the stated
     densities (fp64, r = 5, two-phase slab)."""
