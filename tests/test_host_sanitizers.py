@@ -1,6 +1,6 @@
 """The library's host code (descriptor validation, the build plan, workspace layouts) under
 AddressSanitizer and UndefinedBehaviorSanitizer: every source of dynamis_amd/csrc is
-compiled with the sanitizers on its host side only (-fno-gpu-sanitize; the device code is
+compiled with the sanitizers on its host side only (-Xarch_host; the device code is
 built as usual but never launched) and linked with tests/host_sanitize_main.cpp, which
 calls the host entry points on 20000 random and extreme descriptors (see its header).
 Runs without a GPU; skipped where hipcc is absent."""
@@ -23,9 +23,10 @@ def test_host_code_under_asan_ubsan():
     from dynamis_amd import build as b
 
     with tempfile.TemporaryDirectory() as d:
+        # every sanitizer flag is scoped to the host pass with -Xarch_host
         flags = [f for f in b.FLAGS if f not in ("-O3",)] + ["-O1", "-g", "-fno-omit-frame-pointer",
-                                                          "-fsanitize=address,undefined",
-                                                          "-fno-sanitize-recover=all", "-fno-gpu-sanitize"]
+                                                          "-Xarch_host", "-fsanitize=address,undefined",
+                                                          "-Xarch_host", "-fno-sanitize-recover=all"]
         objs = []
         for src in b.SOURCES:
             obj = os.path.join(d, src + ".o")
@@ -39,7 +40,8 @@ def test_host_code_under_asan_ubsan():
         r = subprocess.run(cmd, capture_output=True, text=True)
         assert r.returncode == 0, r.stdout + r.stderr
         exe = os.path.join(d, "host_sanitize")
-        cmd = [b.HIPCC, f"--offload-arch={b.ARCH}", "-fsanitize=address,undefined", main_o, *objs, "-o", exe]
+        cmd = [b.HIPCC, f"--offload-arch={b.ARCH}", "-fsanitize=address,undefined", "-fno-gpu-sanitize",
+               main_o, *objs, "-o", exe]
         r = subprocess.run(cmd, capture_output=True, text=True)
         assert r.returncode == 0, r.stdout + r.stderr
         env = dict(os.environ, ASAN_OPTIONS="detect_leaks=0", UBSAN_OPTIONS="print_stacktrace=1")
