@@ -308,17 +308,22 @@ def _host_threads():
 
 def cpu_baseline(args, box, n, E_gpu):
     """The C oracle (the reference algorithm with the canonical predicate) on this host:
-    the full build with all the threads the job may use, median of 3; a one-thread run on
-    a bounded sample (every 10th atom as a target, the ``radius_graph_pbc_ex`` path), median
-    of 3; and the Morton SFC keys of all atoms, with all threads and with one, median of 5."""
+    the full build of the benchmarked box with all the threads the job may use, median of
+    5; a one-thread full build, median of 5, of the same box when it has at most 200k atoms,
+    else of C2 (100k atoms: the one-thread build of C3 would take about 18 s per run); and
+    the Morton SFC keys of all atoms, with all threads and with one, median of 5."""
     import numpy as np
 
     import oracle
+    from dynamis_amd import configs
 
     thr, cores = _host_threads()
     if args.cpu_threads:
         thr = args.cpu_threads
-    cell_used = np.asarray(box.cell, np.float64).astype(box.pos.dtype).astype(np.float64)
+
+    def cell_of(b):
+        return np.asarray(b.cell, np.float64).astype(b.pos.dtype).astype(np.float64)
+
     r32 = float(np.float32(box.radius))
 
     def timed(fn, reps):
@@ -330,14 +335,14 @@ def cpu_baseline(args, box, n, E_gpu):
             ts.append(time.perf_counter() - t)
         return float(np.median(ts)), out
 
-    full_s, o = timed(lambda: oracle.radius_graph(box.pos, cell_used, box.pbc, r32,
-                                                  target_indices=box.targets, threads=thr), 3)
+    full_s, o = timed(lambda: oracle.radius_graph(box.pos, cell_of(box), box.pbc, r32,
+                                                  target_indices=box.targets, threads=thr), 5)
     E_cpu = len(o["src"])
     del o
-    sample_t = (np.arange(0, n, 10, dtype=np.int64) if box.targets is None
-                else np.ascontiguousarray(box.targets[::10]))
-    one_s, oc = timed(lambda: oracle.radius_graph(box.pos, cell_used, box.pbc, r32,
-                                                  target_indices=sample_t, threads=1), 3)
+    one_box, one_name = (box, args.config) if n <= 200_000 else (configs.c2(), "C2")
+    one_s, oc = timed(lambda: oracle.radius_graph(one_box.pos, cell_of(one_box), one_box.pbc,
+                                                  float(np.float32(one_box.radius)),
+                                                  target_indices=one_box.targets, threads=1), 5)
     E_one = len(oc["src"])
     del oc
     p32 = box.pos.astype(np.float32)
@@ -347,14 +352,15 @@ def cpu_baseline(args, box, n, E_gpu):
            "kind": "port",
            "sample": f"full build of {args.config} ({n} atoms, {E_cpu} edges) by the C oracle "
                      f"(reference algorithm, fp64 predicate), OpenMP {thr} threads "
-                     f"({cores} cores in this process's affinity), median of 3: "
+                     f"({cores} cores in this process's affinity), median of 5: "
                      f"{full_s * 1e3:.0f} ms",
            "ms_per_rebuild": round(full_s * 1e3, 1),
            "host_cores_affinity": cores,
            "one_thread": {"value": round(E_one / one_s / 1e9, 5), "unit": "Gedges/s", "cores": 1,
-                          "sample": f"every 10th atom as a target ({len(sample_t)} targets, {E_one} "
-                                    f"edges), median of 3: {one_s * 1e3:.0f} ms",
-                          "ms_per_rebuild_extrapolated": round(one_s * E_cpu / max(E_one, 1) * 1e3, 1)},
+                          "config": one_name,
+                          "sample": f"full build of {one_name} ({len(one_box.pos)} atoms, {E_one} edges), "
+                                    f"one thread, median of 5: {one_s * 1e3:.0f} ms",
+                          "ms_per_rebuild": round(one_s * 1e3, 1)},
            "sfc_keys": {"ms": round(keys_s * 1e3, 2), "cores": thr, "ms_one_thread": round(keys1_s * 1e3, 2),
                         "sample": f"Morton keys of all {n} atoms, median of 5 each"}}
     if E_cpu != E_gpu:
@@ -472,7 +478,7 @@ def bench_batch(args):
         def timed(batched):
             # the wrapper with its choice forced either way
             old = wrap._batch_in_one_pass
-            wrap._batch_in_one_pass = lambda natoms: batched
+            wrap._batch_in_one_pass = lambda natoms, *a: batched
             try:
                 for _ in range(max(1, args.warmup)):
                     wrap.radius_graph_pbc_cuda(data, 6.0, 0)
@@ -485,7 +491,7 @@ def bench_batch(args):
             finally:
                 wrap._batch_in_one_pass = old
 
-        chosen = wrap._batch_in_one_pass([int(x) for x in natoms])
+        chosen = wrap._batch_in_one_pass([int(x) for x in natoms], np.array(cells), [True] * 3, 6.0)
         ms_batch, out = timed(True)
         ms_loop, _ = timed(False)
         print(json.dumps({"metric": "radius_graph_pbc_cuda ms per batch", "structures": B,

@@ -2509,6 +2509,12 @@ constexpr int kMaxDevices = 64;
 static __device__ __align__(256) unsigned char scratch[kScratchBytes];
 static std::mutex g_scratch_mu;
 static void* g_scratch_ptr[kMaxDevices];
+// Overlap guard, per device: the stream of the last call and an event recorded behind it.
+// A call on another stream while that event is still pending would share the scratch with
+// work in flight, and is refused.  (Created once per device, with the scratch lookup.)
+static hipEvent_t g_scratch_done[kMaxDevices];
+static hipStream_t g_scratch_stream[kMaxDevices];
+static bool g_scratch_used[kMaxDevices];
 
 // The scratch address on the current device, looked up once per device.
 // The stream must belong to the current device: the address is that device's copy.
@@ -2532,9 +2538,43 @@ static dg_status scratch_on_current_device(hipStream_t s, void** out)
         e = hipGetSymbolAddress(&ptr, HIP_SYMBOL(scratch));
         if (e != hipSuccess || !ptr)
             return fail(DG_ERR_HIP, std::string("hipGetSymbolAddress(scratch): ") + hipGetErrorString(e));
+        e = hipEventCreateWithFlags(&g_scratch_done[dev], hipEventDisableTiming);
+        if (e != hipSuccess)
+            return fail(DG_ERR_HIP, std::string("hipEventCreateWithFlags: ") + hipGetErrorString(e));
         g_scratch_ptr[dev] = ptr;
     }
+    // A stream under capture records no completion to test: such calls are not guarded.
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (s != nullptr) {
+        e = hipStreamIsCapturing(s, &cap);
+        if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipStreamIsCapturing: ") + hipGetErrorString(e));
+    }
+    if (cap == hipStreamCaptureStatusNone && g_scratch_used[dev] && g_scratch_stream[dev] != s) {
+        e = hipEventQuery(g_scratch_done[dev]);
+        if (e == hipErrorNotReady)
+            return fail(DG_ERR_INVALID, "dg_graph_build_noalloc: the previous call on this device (on another "
+                                        "stream) has not completed; calls on different streams share the static "
+                                        "scratch and must not overlap");
+        if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipEventQuery: ") + hipGetErrorString(e));
+    }
     *out = g_scratch_ptr[dev];
+    return DG_OK;
+}
+
+// Marks the end of a call on stream s (current device): the overlap guard's event.
+static dg_status scratch_release(hipStream_t s)
+{
+    int dev = -1;
+    hipError_t e = hipGetDevice(&dev);
+    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
+    hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
+    if (s != nullptr && hipStreamIsCapturing(s, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
+    if (cap != hipStreamCaptureStatusNone) return DG_OK;
+    std::lock_guard<std::mutex> lock(g_scratch_mu);
+    e = hipEventRecord(g_scratch_done[dev], s);
+    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipEventRecord: ") + hipGetErrorString(e));
+    g_scratch_stream[dev] = s;
+    g_scratch_used[dev] = true;
     return DG_OK;
 }
 
@@ -2569,6 +2609,8 @@ extern "C" dg_status dg_graph_build_noalloc(const dg_graph_desc* desc, const voi
     if (st != DG_OK) return st;
     hipLaunchKernelGGL(copy_totals_kernel, dim3(1), dim3(64), 0, s,
                        (const int64_t*)at<int64_t>(ws, p.o_tot), totals_out);
-    return check_launch("dg_graph_build_noalloc");
+    st = check_launch("dg_graph_build_noalloc");
+    if (st != DG_OK) return st;
+    return scratch_release(s);
 }
 #endif  // DG_MAIN_TU

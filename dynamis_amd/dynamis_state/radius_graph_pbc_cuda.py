@@ -18,16 +18,51 @@ from . import dynamis_state_impl as _impl
 # structures of up to 250 atoms in 0.35 ms against 23.4 ms, 512 of up to 500 in 1.5 ms
 # against 92 ms.  A single structure, and structures above BATCH_MAX_ATOMS, always go
 # through the cell-list build.
+#
+# The batched kernel visits, for every atom pair, the periodic shifts S with
+# |frac_t - frac_s - S_d| <= r / d_face on each periodic axis: about prod_d (2 r / d_face + 1)
+# of them.  The per-pair cost above was measured at about 6 such images per pair (250-atom
+# cubes at r = 6 A: r / d_face = 0.41 per axis), so a structure's pairs are weighted by its
+# image count over 6.  A structure needing more than BATCH_MAX_IMAGES images per pair (a
+# cell that is small against the cutoff) sends the batch through the loop, whose cell-list
+# build handles such cells without visiting every image of every pair.
 BATCH_MAX_ATOMS = 8192
+BATCH_MAX_IMAGES = 343.0
 _LOOP_MS_PER_STRUCTURE = 0.19
 _BATCH_MS = 0.22
 _BATCH_MS_PER_PAIR = 1.6e-8
+_BATCH_IMAGES_MEASURED = 6.0
 
 
-def _batch_in_one_pass(natoms) -> bool:
+def _images_per_pair(cell, pbc, radius) -> float:
+    """prod over periodic axes of (2 r / d_face + 1) for one cell (rows = lattice vectors)."""
+    import numpy as np
+
+    c = np.asarray(cell, dtype=np.float64).reshape(3, 3)
+    vol = abs(float(np.dot(c[0], np.cross(c[1], c[2]))))
+    img = 1.0
+    for d in range(3):
+        if not pbc[d]:
+            continue
+        area = float(np.linalg.norm(np.cross(c[(d + 1) % 3], c[(d + 2) % 3])))
+        if vol <= 0.0 or area <= 0.0:
+            return float("inf")
+        img *= 2.0 * float(radius) / (vol / area) + 1.0
+    return img
+
+
+def _batch_in_one_pass(natoms, cells=None, pbc=(True, True, True), radius=6.0) -> bool:
+    """Whether the batched build is expected to beat the per-structure loop.  Without
+    ``cells`` every structure is costed at the measured image count."""
     if len(natoms) < 2 or max(natoms) > BATCH_MAX_ATOMS:
         return False
-    pairs = sum(n * n for n in natoms)
+    if cells is None:
+        weights = [1.0] * len(natoms)
+    else:
+        weights = [_images_per_pair(c, pbc, radius) / _BATCH_IMAGES_MEASURED for c in cells]
+        if max(weights) * _BATCH_IMAGES_MEASURED > BATCH_MAX_IMAGES:
+            return False
+    pairs = sum(n * n * w for n, w in zip(natoms, weights))
     return _BATCH_MS + _BATCH_MS_PER_PAIR * pairs < _LOOP_MS_PER_STRUCTURE * len(natoms)
 
 
@@ -60,7 +95,9 @@ def radius_graph_pbc_cuda(data, radius: float, max_num_neighbors_threshold: int,
                                       enforce_max_neighbors_strictly)
 
     natoms = [int(x) for x in data.natoms.tolist()]
-    if _batch_in_one_pass(natoms):
+    pbc_list = [bool(x) for x in pbc_flags.tolist()]
+    if _batch_in_one_pass(natoms, data.cell.detach().to("cpu", torch.float64).numpy(), pbc_list,
+                          float(radius)):
         return _impl.build_batch(data.pos, data.cell, data.natoms, pbc_flags, float(radius),
                                  int(max_num_neighbors_threshold))
 

@@ -93,7 +93,7 @@ def test_wrapper_uses_the_batch_and_matches_the_loop(cuda, monkeypatch):
     data = types.SimpleNamespace(pos=torch.from_numpy(pos).to(cuda), cell=torch.from_numpy(cells).to(cuda),
                                  natoms=torch.from_numpy(natoms).to(cuda),
                                  pbc=torch.tensor([pbc] * len(natoms)).to(cuda))
-    assert wrap._batch_in_one_pass([int(x) for x in natoms])
+    assert wrap._batch_in_one_pass([int(x) for x in natoms], cells, pbc, r)
     ei, co, nn = wrap.radius_graph_pbc_cuda(data, r, 0)
     monkeypatch.setattr(wrap, "BATCH_MAX_ATOMS", 0)  # force the per-structure loop
     ei2, co2, nn2 = wrap.radius_graph_pbc_cuda(data, r, 0)
@@ -125,3 +125,36 @@ def test_batch_errors(cuda):
     ei, co, nn = impl.build_batch(p, torch.from_numpy(cells), torch.from_numpy(natoms), torch.tensor(pbc), r)
     assert int(nn.sum()) == ei.shape[1]
     assert torch.equal(ei, ei2) and torch.equal(co, co2) and torch.equal(nn, nn2)
+
+
+def test_edge_order_of_each_wrapper_path(cuda, monkeypatch):
+    """The two paths of radius_graph_pbc_cuda order edges differently, both as documented:
+    the batched build by (target, source, shift) ascending, structure after structure; the
+    per-structure loop exactly as the single-structure builds, concatenated with batch
+    offsets (targets in cell-list order)."""
+    natoms, cells, pbc, r, pos = _batch(101)
+    while len(natoms) < 16:
+        n2, c2, _, _, p2 = _batch(102 + len(natoms))
+        natoms, cells = np.r_[natoms, n2], np.concatenate([cells, c2])
+        pos = np.concatenate([pos, p2.astype(pos.dtype)])
+    data = types.SimpleNamespace(pos=torch.from_numpy(pos).to(cuda), cell=torch.from_numpy(cells).to(cuda),
+                                 natoms=torch.from_numpy(natoms).to(cuda),
+                                 pbc=torch.tensor([pbc] * len(natoms)).to(cuda))
+    print(f"\n[case] wrapper order B={len(natoms)} N={len(pos)}", flush=True)
+    ei, co, nn = wrap.radius_graph_pbc_cuda(data, r, 0)
+    e = ei.cpu().numpy()
+    c = co.cpu().numpy().astype(np.int64)
+    keys = np.stack([e[1], e[0], c[:, 0], c[:, 1], c[:, 2]])
+    order = np.lexsort(keys[::-1])
+    assert np.array_equal(order, np.arange(e.shape[1]))  # already (dst, src, S) ascending
+    monkeypatch.setattr(wrap, "BATCH_MAX_ATOMS", 0)  # the per-structure loop
+    ei2, co2, nn2 = wrap.radius_graph_pbc_cuda(data, r, 0)
+    off = np.r_[0, np.cumsum(natoms)]
+    parts_e, parts_c = [], []
+    for b in range(len(natoms)):
+        sl = slice(off[b], off[b + 1])
+        e1, c1, _ = impl.radius_graph_pbc(data.pos[sl], data.cell[b], torch.tensor(pbc), r, 0, False)
+        parts_e.append(e1 + int(off[b]))
+        parts_c.append(c1)
+    assert torch.equal(ei2, torch.cat(parts_e, 1)) and torch.equal(co2, torch.cat(parts_c, 0))
+    assert torch.equal(nn, nn2)

@@ -122,3 +122,84 @@ def test_no_alloc_capacity_and_limit(cuda):
                                     None, None, L.DG_F32, L.ptr(tot), L.stream_of(cuda))
     assert st == L.DG_ERR_WORKSPACE
     assert b"static scratch" in lib.dg_last_error()
+
+
+def test_no_alloc_at_the_scratch_limit(cuda):
+    # the largest uniform box whose workspace still fits the 64 MiB scratch, byte for byte
+    lib = L.lib()
+
+    def box_of(n):
+        return configs.uniform(n, seed=35, dtype=np.float32)
+
+    def wsb(n):
+        d, *_ = _desc(box_of(n), torch.device("cpu"))
+        return lib.dg_graph_workspace_size(d)
+
+    lo, hi = 50_000, 400_000
+    while hi - lo > 1:
+        m = (lo + hi) // 2
+        lo, hi = (m, hi) if wsb(m) <= (64 << 20) else (lo, m)
+    assert (64 << 20) - wsb(lo) < (1 << 20) < wsb(lo + 1) - (64 << 20) + (1 << 20)
+    box = box_of(lo)
+    print(f"\n[case] noalloc at the limit N={lo} workspace={wsb(lo)}", flush=True)
+    E, *_ = _with_workspace(box, cuda, int(lo * 100))
+    cap = E + 64
+    E, fl, ei, sh, cnt = _with_workspace(box, cuda, cap)
+    E2, fl2, ei2, sh2, cnt2 = _no_alloc(box, cuda, cap)
+    assert (E2, fl2) == (E, fl) and E > 0
+    assert torch.equal(cnt2, cnt) and torch.equal(ei2, ei) and torch.equal(sh2, sh)
+    # one atom more does not fit
+    d, pos, _ = _desc(box_of(lo + 1), cuda)
+    tot = torch.zeros(2, dtype=torch.int64, device=cuda)
+    st = lib.dg_graph_build_noalloc(d, L.ptr(pos), None, 16, None, L.ptr(tot), L.ptr(tot), L.ptr(tot),
+                                    None, None, L.DG_F32, L.ptr(tot), L.stream_of(cuda))
+    assert st == L.DG_ERR_WORKSPACE
+
+
+def test_no_alloc_explicit_targets_with_vectors(cuda):
+    # random explicit targets (the target sort path) with edge vectors: two calls, the
+    # second smaller
+    rng = np.random.default_rng(36)
+    for n, nt in [(30000, 11000), (8000, 900)]:
+        box = configs.uniform(n, seed=37 + n, dtype=np.float32)
+        box.targets = rng.permutation(rng.choice(n, nt, replace=False)).astype(np.int64)
+        print(f"\n[case] noalloc targets + vectors N={n} nt={nt}", flush=True)
+        E, *_ = _with_workspace(box, cuda, int(nt * 100))
+        cap = E + 64
+        E, fl, ei, sh, cnt, vec, dist = _with_workspace(box, cuda, cap, vectors=True)
+        E2, fl2, ei2, sh2, cnt2, vec2, dist2 = _no_alloc(box, cuda, cap, vectors=True)
+        assert (E2, fl2) == (E, fl) and E > 0
+        assert torch.equal(cnt2, cnt) and torch.equal(ei2, ei) and torch.equal(sh2, sh)
+        assert torch.equal(vec2, vec) and torch.equal(dist2, dist)
+
+
+def test_no_alloc_refuses_an_overlapping_call(cuda):
+    # a call on stream B while the previous call's work on stream A is still pending
+    # (held back behind a bounded spin kernel) is refused; once A has drained, B may call
+    lib = L.lib()
+    box = configs.uniform(9000, seed=32, dtype=np.float32)
+    E, *_ = _with_workspace(box, cuda, 9000 * 100)
+    d, pos, _ = _desc(box, cuda)
+    ei, sh, cnt = _outputs(E + 64, len(box.pos), cuda)
+    tot = torch.zeros(2, dtype=torch.int64, device=cuda)
+    a, b = torch.cuda.Stream(cuda), torch.cuda.Stream(cuda)
+    torch.cuda.synchronize()
+
+    def call(stream):
+        s = L.ctypes.c_void_p(stream.cuda_stream)
+        return lib.dg_graph_build_noalloc(d, L.ptr(pos), None, E + 64, L.ptr(cnt),
+                                          L.ctypes.c_void_p(ei.data_ptr()),
+                                          L.ctypes.c_void_p(ei.data_ptr() + 8 * (E + 64)), L.ptr(sh),
+                                          None, None, L.DG_F32, L.ptr(tot), s)
+
+    print("\n[case] noalloc overlap guard", flush=True)
+    with torch.cuda.stream(a):
+        torch.cuda._sleep(200_000_000)  # ~0.1 s of spinning on stream A
+    assert call(a) == L.DG_OK
+    assert call(a) == L.DG_OK  # the same stream is ordered: allowed
+    assert call(b) == L.DG_ERR_INVALID
+    assert b"has not completed" in lib.dg_last_error()
+    torch.cuda.synchronize()
+    assert call(b) == L.DG_OK
+    torch.cuda.synchronize()
+    assert int(tot[0]) == E
