@@ -7,10 +7,11 @@
 //                      with x at bit 0 (fp32 arithmetic)
 //   Hilbert :62-109    order-7 quantisation with the reference's per-bit transform
 //   labels  :114-173   unweighted closed form / exact int64 weighted cut
-// The sort replaces at::sort (sfc_kernels.cu:224) with a stable 8-bit LSD radix sort whose
-// pass count adapts to the key bits that actually vary.
+// The sort replaces at::sort (sfc_kernels.cu:224) with a stable 8-bit LSD radix sort that
+// skips, on the device, the bytes in which all keys agree.
 #include <hip/hip_runtime.h>
 #include <math.h>
+#include <stddef.h>
 #include <stdint.h>
 #include <string.h>
 
@@ -145,27 +146,44 @@ __global__ void keys_kernel(const float* __restrict__ pos, int64_t n, int curve,
 }
 
 // ------------------------------------------------------------------ radix sort
-// Stable LSD radix sort, 8 bits per pass, with passes only over the key bytes that vary
-// (the OR and AND of all keys, folded per workgroup on the device and across workgroups
-// on the host).  Per pass: rs_hist_kernel counts each tile's digits (digit-major,
-// hist[d * nblocks + b]); a scan of those counts gives every tile its place within every
-// digit; rs_scatter_kernel ranks its tile's keys stably (index order within a digit),
-// reorders them by digit in LDS and writes each digit's run contiguously, keys and then
-// positions.  Keys are kept with the sign bit flipped between passes (so they order as
-// unsigned); positions are int32 inside the sort, and the last pass writes them into the
-// int64 permutation.
+// Stable LSD radix sort, 8 bits per pass, with no host synchronisation, so a call is a
+// fixed sequence of launches that a HIP graph can capture:
+//   rs_span_kernel       the OR and AND of the keys, per workgroup;
+//   rs_plan_kernel       one workgroup: the pass plan -- a byte in which every key has the
+//                        same digit is skipped (its kernels exit at once), the first pass
+//                        that runs reads the caller's keys, the last writes the int64
+//                        permutation;
+//   per byte q = 0..7:
+//     rs_hist_kernel<q>  each tile's digit counts, digit-major (hist[d * ntiles + t]);
+//     device scan of hist (digit-major: each tile's output base per digit)
+//     rs_pass_kernel<q>  each tile ranks its keys stably by digit (eight ballots per 64
+//                        keys and per-wave running counts) and writes each digit's run
+//                        contiguously through LDS: keys and int32 positions, or, in the last
+//                        pass, the int64 permutation.
+// Keys are kept with the sign bit flipped inside the sort (so they order as unsigned).
 constexpr int kRsBlock = 256;
 constexpr int kRsPer = 16;                     // keys per thread
 constexpr int kRsTile = kRsBlock * kRsPer;     // keys per tile
 constexpr int kRsWaveKeys = 64 * kRsPer;       // a wave's contiguous share of a tile
-constexpr int kSpanBlocks = 512;               // workgroups of the key span
+constexpr int kRsPasses = 8;
+constexpr int kRsSpanBlocks = 512;             // workgroups of the key span (at most)
 
 __device__ __forceinline__ uint64_t ukey(int64_t k) { return (uint64_t)k ^ 0x8000000000000000ull; }
 __device__ __forceinline__ int digit_of(uint64_t k, int shift) { return (int)((k >> shift) & 0xffu); }
 
-// OR and AND of the (sign-flipped) keys: one pair per workgroup, folded on the host
-__global__ __launch_bounds__(256) void key_span_kernel(const int64_t* __restrict__ keys, int64_t n,
-                                                       unsigned long long* __restrict__ part)
+// What pass q does (written by rs_plan_kernel): run = 0 skips it; src / dst: 0 the
+// caller's keys, 1 and 2 the two key / position buffers, 3 the permutation.
+struct RsPass {
+    int run, src, dst, pad;
+};
+struct RsCtl {
+    RsPass pass[kRsPasses];
+    int none;  // every key equal: the permutation is the identity
+};
+
+// OR and AND of the (sign-flipped) keys: one pair per workgroup.
+__global__ __launch_bounds__(256) void rs_span_kernel(const int64_t* __restrict__ keys, int64_t n,
+                                                      unsigned long long* __restrict__ part)
 {
     unsigned long long o = 0, a = ~0ull;
     for (int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x; i < n;
@@ -194,31 +212,74 @@ __global__ __launch_bounds__(256) void key_span_kernel(const int64_t* __restrict
     }
 }
 
-// FIRST: the caller's keys (signed); later passes read sign-flipped keys.
-template <bool FIRST>
-__device__ __forceinline__ uint64_t load_key(const int64_t* kin, int64_t i)
+// One workgroup: folds the span partials and writes the pass plan (a byte in which every
+// key has the same digit is skipped).
+__global__ __launch_bounds__(256) void rs_plan_kernel(const unsigned long long* __restrict__ part, int nparts,
+                                                      RsCtl* __restrict__ ctl)
 {
-    return FIRST ? ukey(kin[i]) : (uint64_t)kin[i];
+    unsigned long long o = 0, a = ~0ull;
+    for (int b = threadIdx.x; b < nparts; b += blockDim.x) {
+        o |= part[2 * b];
+        a &= part[2 * b + 1];
+    }
+    for (int m = 32; m > 0; m >>= 1) {
+        o |= (unsigned long long)__shfl_xor((long long)o, m, 64);
+        a &= (unsigned long long)__shfl_xor((long long)a, m, 64);
+    }
+    __shared__ unsigned long long s_o[4], s_a[4];
+    if ((threadIdx.x & 63) == 0) {
+        s_o[threadIdx.x >> 6] = o;
+        s_a[threadIdx.x >> 6] = a;
+    }
+    __syncthreads();
+    if (threadIdx.x == 0) {
+        for (int w = 1; w < (int)(blockDim.x >> 6); ++w) {
+            o |= s_o[w];
+            a &= s_a[w];
+        }
+        const unsigned long long vary = o & ~a;
+        int last = -1;
+        for (int p = 0; p < kRsPasses; ++p)
+            if ((vary >> (8 * p)) & 0xffull) last = p;
+        int cur = 0;  // where the data is before the next pass that runs
+        for (int p = 0; p < kRsPasses; ++p) {
+            RsPass q = {0, 0, 0, 0};
+            if ((vary >> (8 * p)) & 0xffull) {
+                q.run = 1;
+                q.src = cur;
+                q.dst = p == last ? 3 : (cur == 1 ? 2 : 1);
+                cur = q.dst;
+            }
+            ctl->pass[p] = q;
+        }
+        ctl->none = last < 0 ? 1 : 0;
+    }
 }
 
-// Digit counts of every tile of kRsTile keys, stored digit-major: hist[d * nblocks + b].
-// (One-workgroup scans of these counts -- the last workgroup to finish walking the digit
-// columns -- measured 5x slower than the three-kernel device scan: the walk is latency-bound.)
-template <bool FIRST>
-__global__ __launch_bounds__(kRsBlock) void rs_hist_kernel(const int64_t* __restrict__ kin, int64_t n,
-                                                           int shift, int* __restrict__ hist, int nblocks)
+// Digit counts of byte Q of every tile of the pass's input, digit-major.
+template <int Q>
+__global__ __launch_bounds__(kRsBlock) void rs_hist_kernel(const int64_t* __restrict__ ukeys, int64_t n,
+                                                           const int64_t* __restrict__ kb1,
+                                                           const int64_t* __restrict__ kb2,
+                                                           const RsCtl* __restrict__ ctl, int* __restrict__ hist)
 {
+    const RsPass P = ctl->pass[Q];
+    if (!P.run) return;
     __shared__ int h[256];
     h[threadIdx.x] = 0;
     __syncthreads();
+    const int64_t* kin = P.src == 1 ? kb1 : kb2;
     const int64_t base = (int64_t)blockIdx.x * kRsTile;
 #pragma unroll 4
     for (int u = 0; u < kRsPer; ++u) {
         const int64_t i = base + u * kRsBlock + threadIdx.x;
-        if (i < n) atomicAdd(&h[digit_of(load_key<FIRST>(kin, i), shift)], 1);
+        if (i < n) {
+            const uint64_t k = P.src == 0 ? ukey(ukeys[i]) : (uint64_t)kin[i];
+            atomicAdd(&h[digit_of(k, 8 * Q)], 1);
+        }
     }
     __syncthreads();
-    hist[threadIdx.x * nblocks + blockIdx.x] = h[threadIdx.x];
+    hist[(int64_t)threadIdx.x * gridDim.x + blockIdx.x] = h[threadIdx.x];
 }
 
 struct RsScatterLds {
@@ -227,29 +288,38 @@ struct RsScatterLds {
         int32_t v[kRsTile];   // then their positions
     } buf;
     uint8_t dig[kRsTile];      // the digit of every slot
-    int start[256];            // first slot of each digit
     int glob[256];             // output index of slot 0 of each digit's run, for this tile
     int wc[kRsBlock / 64][256];  // per wave: running count per digit, then its first slot
     int w32[kRsBlock / 64];
 };
 
-// One tile: stable slots by digit (wave w holds keys [w kRsWaveKeys, (w + 1) kRsWaveKeys)
-// of the tile, 64 per round; a key's rank among its wave's equal digits comes from eight
-// ballots per round and the wave's running count), then the reorder through LDS and the
-// contiguous write of every digit's run.  FIRST: positions are the keys' indices; LAST:
-// positions go to perm (int64) and the keys are not written.
-template <bool FIRST, bool LAST>
-__global__ __launch_bounds__(kRsBlock) void rs_scatter_kernel(
-    const int64_t* __restrict__ kin, const int32_t* __restrict__ vin, int64_t n, int shift,
-    const int* __restrict__ offs, int nblocks, int64_t* __restrict__ kout, int32_t* __restrict__ vout,
-    int64_t* __restrict__ perm)
+// Pass over byte Q.  offs: the exclusive scan of this pass's tile counts (digit-major).
+template <int Q>
+__global__ __launch_bounds__(kRsBlock) void rs_pass_kernel(
+    const int64_t* __restrict__ ukeys, int64_t n, int64_t* __restrict__ kb1, int64_t* __restrict__ kb2,
+    int32_t* __restrict__ vb1, int32_t* __restrict__ vb2, int64_t* __restrict__ perm,
+    const RsCtl* __restrict__ ctl, const int* __restrict__ offs)
 {
+    constexpr int shift = 8 * Q;
+    const RsPass P = ctl->pass[Q];
+    if (Q == 0 && ctl->none) {  // every key equal: the identity
+        for (int64_t i = (int64_t)blockIdx.x * kRsBlock + threadIdx.x; i < n; i += (int64_t)gridDim.x * kRsBlock)
+            perm[i] = i;
+        return;
+    }
+    if (!P.run) return;
     __shared__ RsScatterLds S;
+    const bool first = P.src == 0, last = P.dst == 3;
+    const int64_t* kin = P.src == 1 ? kb1 : kb2;
+    const int32_t* vin = P.src == 1 ? vb1 : vb2;
+    int64_t* kout = P.dst == 1 ? kb1 : kb2;
+    int32_t* vout = P.dst == 1 ? vb1 : vb2;
     const int lane = threadIdx.x & 63, w = threadIdx.x >> 6;
-    const int64_t base = (int64_t)blockIdx.x * kRsTile;
-    const int m = (int)((n - base) < kRsTile ? (n - base) : kRsTile);  // keys in this tile
+    const int t = blockIdx.x, ntiles = gridDim.x;
     for (int k = 0; k < kRsBlock / 64; ++k) S.wc[k][threadIdx.x] = 0;
     __syncthreads();
+    const int64_t base = (int64_t)t * kRsTile;
+    const int m = (int)((n - base) < kRsTile ? (n - base) : kRsTile);  // keys in this tile
     uint64_t key[kRsPer];
     int32_t val[kRsPer];
     int rk[kRsPer];
@@ -258,9 +328,12 @@ __global__ __launch_bounds__(kRsBlock) void rs_scatter_kernel(
     for (int u = 0; u < kRsPer; ++u) {
         const int i = w * kRsWaveKeys + u * 64 + lane;
         const bool valid = i < m;
-        key[u] = valid ? load_key<FIRST>(kin, base + i) : 0ull;
-        val[u] = valid ? (FIRST ? (int32_t)(base + i) : vin[base + i]) : 0;
+        key[u] = valid ? (first ? ukey(ukeys[base + i]) : (uint64_t)kin[base + i]) : 0ull;
+        val[u] = valid ? (first ? (int32_t)(base + i) : vin[base + i]) : 0;
     }
+    // this tile's output base per digit (independent of the ranking below, so its load
+    // overlaps it): the keys of lower digits plus this digit's keys in the tiles before
+    const int before_t = offs[(int64_t)threadIdx.x * ntiles + t];
 #pragma unroll
     for (int u = 0; u < kRsPer; ++u) {
         const int i = w * kRsWaveKeys + u * 64 + lane;
@@ -284,8 +357,8 @@ __global__ __launch_bounds__(kRsBlock) void rs_scatter_kernel(
         rk[u] = before + inwave;
     }
     __syncthreads();
-    // thread d: the digit's count and start in the tile, each wave's first slot of it, and
-    // where slot 0 of the digit's run lands in the output
+    // thread d: the digit's start in the tile, each wave's first slot of it, and where
+    // slot 0 of the digit's run lands in the output
     {
         const int d = threadIdx.x;
         int c = 0;
@@ -298,8 +371,7 @@ __global__ __launch_bounds__(kRsBlock) void rs_scatter_kernel(
             S.wc[k][d] = at;
             at += ck;
         }
-        S.start[d] = ex;
-        S.glob[d] = offs[(int64_t)d * nblocks + blockIdx.x] - ex;
+        S.glob[d] = before_t - ex;
     }
     __syncthreads();
     int slot[kRsPer];
@@ -315,7 +387,7 @@ __global__ __launch_bounds__(kRsBlock) void rs_scatter_kernel(
         }
     }
     __syncthreads();
-    if constexpr (!LAST)
+    if (!last)
         for (int sl = threadIdx.x; sl < m; sl += kRsBlock) kout[S.glob[S.dig[sl]] + sl] = (int64_t)S.buf.k[sl];
     __syncthreads();
 #pragma unroll
@@ -324,17 +396,11 @@ __global__ __launch_bounds__(kRsBlock) void rs_scatter_kernel(
     __syncthreads();
     for (int sl = threadIdx.x; sl < m; sl += kRsBlock) {
         const int64_t dst = S.glob[S.dig[sl]] + sl;
-        if constexpr (LAST)
+        if (last)
             perm[dst] = (int64_t)S.buf.v[sl];
         else
             vout[dst] = S.buf.v[sl];
     }
-}
-
-__global__ void iota_kernel(int64_t n, int64_t* __restrict__ out)
-{
-    int64_t i = (int64_t)blockIdx.x * blockDim.x + threadIdx.x;
-    if (i < n) out[i] = i;
 }
 
 // ------------------------------------------------------------------ labels
@@ -664,8 +730,8 @@ dg_status launch_ok(const char* what)
 }
 
 struct SortLayout {
-    size_t o_k0, o_v0, o_k1, o_v1, o_hist, o_offs, o_part, o_span, total;
-    int nblocks, nspan;
+    size_t o_k0, o_v0, o_k1, o_v1, o_part, o_ctl, o_hist, o_offs, o_spart, total;
+    int nblocks, nparts;
 };
 
 SortLayout sort_layout(int64_t n)
@@ -675,16 +741,17 @@ SortLayout sort_layout(int64_t n)
     auto take = [&](size_t b) { size_t r = o; o = al(o + (b ? b : 1)); return r; };
     L.nblocks = (int)((n + kRsTile - 1) / kRsTile);
     if (L.nblocks < 1) L.nblocks = 1;
-    size_t nh = (size_t)L.nblocks * 256;
-    L.nspan = (int)std::min<int64_t>(kSpanBlocks, std::max<int64_t>(1, (n + 255) / 256));
+    L.nparts = (int)std::min<int64_t>(kRsSpanBlocks, std::max<int64_t>(1, (n + 255) / 256));
+    const size_t nh = (size_t)L.nblocks * 256;
     L.o_k0 = take(8 * n);
     L.o_v0 = take(4 * n);
     L.o_k1 = take(8 * n);
     L.o_v1 = take(4 * n);
+    L.o_part = take(16 * (size_t)L.nparts);
+    L.o_ctl = take(sizeof(RsCtl));
     L.o_hist = take(4 * nh);
     L.o_offs = take(4 * (nh + 1));
-    L.o_part = take(4 * (nh / kScanTile + 2));
-    L.o_span = take(16 * (size_t)L.nspan);
+    L.o_spart = take(4 * (nh / kScanTile + 2));
     L.total = o;
     return L;
 }
@@ -746,60 +813,37 @@ dg_status dg_sfc_order(const int64_t* keys, int64_t n, int64_t* perm, void* ws, 
     if (n < 0) return fail(DG_ERR_INVALID, "n < 0");
     if (n == 0) return DG_OK;
     if (n > 0x7ffffff0LL) return fail(DG_ERR_INVALID, "n too large");
+    if (!keys || !perm) return fail(DG_ERR_INVALID, "keys / perm is NULL");
     SortLayout L = sort_layout(n);
     if (ws_bytes < L.total) return fail(DG_ERR_WORKSPACE, "workspace too small");
     char* w = (char*)ws;
-    unsigned long long* span = (unsigned long long*)(w + L.o_span);
-    hipLaunchKernelGGL(key_span_kernel, dim3((unsigned)L.nspan), dim3(256), 0, s, keys, n, span);
-    std::vector<unsigned long long> h(2 * (size_t)L.nspan);
-    hipError_t e = hipMemcpyAsync(h.data(), span, 16 * (size_t)L.nspan, hipMemcpyDeviceToHost, s);
-    if (e == hipSuccess) e = hipStreamSynchronize(s);
-    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("dg_sfc_order: ") + hipGetErrorString(e));
-    unsigned long long o = 0, a = ~0ull;
-    for (int b = 0; b < L.nspan; ++b) {
-        o |= h[2 * b];
-        a &= h[2 * b + 1];
-    }
-    const unsigned long long vary = o & ~a;
-    int shifts[8], npass = 0;
-    for (int sh = 0; sh < 64; sh += 8)
-        if ((vary >> sh) & 0xffull) shifts[npass++] = sh;
-    if (npass == 0) {
-        // all keys equal: identity permutation
-        hipLaunchKernelGGL(iota_kernel, dim3(nblk(n)), dim3(256), 0, s, n, perm);
-        return launch_ok("dg_sfc_order");
-    }
-    int64_t* kb[2] = {(int64_t*)(w + L.o_k0), (int64_t*)(w + L.o_k1)};
-    int32_t* vb[2] = {(int32_t*)(w + L.o_v0), (int32_t*)(w + L.o_v1)};
+    int64_t* kb1 = (int64_t*)(w + L.o_k0);
+    int64_t* kb2 = (int64_t*)(w + L.o_k1);
+    int32_t* vb1 = (int32_t*)(w + L.o_v0);
+    int32_t* vb2 = (int32_t*)(w + L.o_v1);
+    unsigned long long* part = (unsigned long long*)(w + L.o_part);
+    RsCtl* ctl = (RsCtl*)(w + L.o_ctl);
     int* hist = (int*)(w + L.o_hist);
     int* offs = (int*)(w + L.o_offs);
-    const int64_t nh = (int64_t)L.nblocks * 256;
+    hipLaunchKernelGGL(rs_span_kernel, dim3((unsigned)L.nparts), dim3(256), 0, s, keys, n, part);
+    hipLaunchKernelGGL(rs_plan_kernel, dim3(1), dim3(256), 0, s, (const unsigned long long*)part, L.nparts, ctl);
     const dim3 grid((unsigned)L.nblocks), blk(kRsBlock);
-    for (int q = 0; q < npass; ++q) {
-        const bool first = q == 0, last = q == npass - 1;
-        const int64_t* kin = first ? keys : kb[(q - 1) & 1];
-        const int32_t* vin = first ? nullptr : vb[(q - 1) & 1];
-        int64_t* kout = kb[q & 1];
-        int32_t* vout = vb[q & 1];
-        const int sh = shifts[q];
-        if (first)
-            hipLaunchKernelGGL(rs_hist_kernel<true>, grid, blk, 0, s, kin, n, sh, hist, L.nblocks);
-        else
-            hipLaunchKernelGGL(rs_hist_kernel<false>, grid, blk, 0, s, kin, n, sh, hist, L.nblocks);
-        excl_scan<int, int>(hist, nh, offs, (int*)(w + L.o_part), s);
-        if (first && last)
-            hipLaunchKernelGGL((rs_scatter_kernel<true, true>), grid, blk, 0, s, kin, vin, n, sh,
-                               (const int*)offs, L.nblocks, kout, vout, perm);
-        else if (first)
-            hipLaunchKernelGGL((rs_scatter_kernel<true, false>), grid, blk, 0, s, kin, vin, n, sh,
-                               (const int*)offs, L.nblocks, kout, vout, perm);
-        else if (last)
-            hipLaunchKernelGGL((rs_scatter_kernel<false, true>), grid, blk, 0, s, kin, vin, n, sh,
-                               (const int*)offs, L.nblocks, kout, vout, perm);
-        else
-            hipLaunchKernelGGL((rs_scatter_kernel<false, false>), grid, blk, 0, s, kin, vin, n, sh,
-                               (const int*)offs, L.nblocks, kout, vout, perm);
-    }
+    // (a skipped pass's scan runs over stale counts; nothing reads its result)
+#define DG_RS_PASS(q)                                                                                  \
+    hipLaunchKernelGGL(rs_hist_kernel<q>, grid, blk, 0, s, keys, n, (const int64_t*)kb1, (const int64_t*)kb2, \
+                       (const RsCtl*)ctl, hist);                                                         \
+    excl_scan<int, int>(hist, (int64_t)L.nblocks * 256, offs, (int*)(w + L.o_spart), s);               \
+    hipLaunchKernelGGL(rs_pass_kernel<q>, grid, blk, 0, s, keys, n, kb1, kb2, vb1, vb2, perm,           \
+                       (const RsCtl*)ctl, (const int*)offs)
+    DG_RS_PASS(0);
+    DG_RS_PASS(1);
+    DG_RS_PASS(2);
+    DG_RS_PASS(3);
+    DG_RS_PASS(4);
+    DG_RS_PASS(5);
+    DG_RS_PASS(6);
+    DG_RS_PASS(7);
+#undef DG_RS_PASS
     return launch_ok("dg_sfc_order");
 }
 

@@ -225,9 +225,12 @@ dg_status dg_sfc_keys(const float* pos, int64_t n, int32_t curve, int64_t* keys,
                       size_t workspace_bytes, hipStream_t stream);
 
 /* Stable ascending sort permutation of int64 keys (ties keep index order).
- * Replaces at::sort(sfc_keys) in sfc_kernels.cu:224.  perm int64 [n]. */
+ * Replaces at::sort(sfc_keys) in sfc_kernels.cu:224.  perm int64 [n].  No host
+ * synchronisation: a fixed sequence of launches on the stream (a HIP graph can capture
+ * it); key bytes in which all keys agree are skipped on the device. */
 dg_status dg_sfc_order(const int64_t* keys, int64_t n, int64_t* perm, void* workspace,
                        size_t workspace_bytes, hipStream_t stream);
+
 
 /* Partition labels from a permutation: unweighted closed form (sfc_kernels.cu:114-136)
  * or exact int64 weighted cut (sfc_kernels.cu:153-173, weights int64 [n] or NULL).

@@ -68,3 +68,47 @@ def test_build_replays_in_a_graph(cuda, name):
         assert Eg == Ee and 0 < Eg <= cap, (rep, Eg, Ee)
         assert torch.equal(g_cnt, e_cnt)
         assert torch.equal(g_ei[:, :Eg], e_ei[:, :Ee]) and torch.equal(g_sh[:Eg], e_sh[:Ee])
+
+
+def test_sfc_order_replays_in_a_graph(cuda):
+    """dg_sfc_order (keys -> stable permutation) captured once and replayed over new keys
+    written in place between the replays: it has no host synchronisation (the passes it
+    needs are chosen on the device), so every replay must equal the eager order and a
+    stable argsort, including replays whose keys vary in other bytes than the captured
+    call's keys did."""
+    lib = L.lib()
+    n = 250_003
+    rng = np.random.default_rng(77)
+    keys = torch.from_numpy(rng.integers(0, 2 ** 21, n).astype(np.int64)).to(cuda)
+    wsb = lib.dg_sfc_workspace_size(n)
+    g_ws = torch.empty(wsb, dtype=torch.uint8, device=cuda)
+    g_perm = torch.full((n,), -1, dtype=torch.int64, device=cuda)
+
+    def order(ws, perm):
+        L.check(lib.dg_sfc_order(L.ptr(keys), n, L.ptr(perm), L.ptr(ws), wsb, L.stream_of(cuda)), "dg_sfc_order")
+
+    side = torch.cuda.Stream(device=cuda)
+    side.wait_stream(torch.cuda.current_stream(cuda))
+    with torch.cuda.stream(side):
+        order(g_ws, g_perm)
+    torch.cuda.current_stream(cuda).wait_stream(side)
+    torch.cuda.synchronize()
+    graph = torch.cuda.CUDAGraph()
+    with torch.cuda.graph(graph):
+        order(g_ws, g_perm)
+    torch.cuda.synchronize()
+    e_ws = torch.empty(wsb, dtype=torch.uint8, device=cuda)
+    e_perm = torch.empty(n, dtype=torch.int64, device=cuda)
+    cases = [rng.integers(0, 2 ** 21, n), rng.integers(-2 ** 62, 2 ** 62, n), np.full(n, -5),
+             rng.integers(0, 3, n) << 40, rng.integers(-2 ** 20, 2 ** 20, n) * 7]
+    for rep, k in enumerate(cases):
+        print(f"\n[case] sfc order graph replay {rep}", flush=True)
+        keys.copy_(torch.from_numpy(np.asarray(k, np.int64)))
+        torch.cuda.synchronize()
+        graph.replay()
+        torch.cuda.synchronize()
+        order(e_ws, e_perm)
+        torch.cuda.synchronize()
+        want = np.argsort(np.asarray(k, np.int64), kind="stable")
+        assert np.array_equal(g_perm.cpu().numpy(), want), rep
+        assert torch.equal(g_perm, e_perm)

@@ -33,7 +33,28 @@ def test_keys_degenerate_axis(cuda):
         assert np.array_equal(k, want)
 
 
-@pytest.mark.parametrize("n", [1, 1000, 300_001])
+@pytest.mark.parametrize("n", [1, 4095, 4096, 4097, 65536 * 3 + 17])
+@pytest.mark.parametrize("kind", ["one byte", "two far bytes", "sign", "top byte", "all bytes"])
+def test_order_varying_bytes(cuda, n, kind):
+    # keys that vary in chosen bytes only: the device-side pass plan skips the others
+    print(f"\n[case] sfc order bytes n={n} {kind}", flush=True)
+    rng = np.random.default_rng(n + len(kind))
+    if kind == "one byte":
+        keys = rng.integers(0, 256, n) << 16
+    elif kind == "two far bytes":
+        keys = (rng.integers(0, 256, n) << 8) | (rng.integers(0, 4, n) << 48) | (123 << 24)
+    elif kind == "sign":
+        keys = rng.integers(-3, 3, n)
+    elif kind == "top byte":
+        keys = rng.integers(-128, 127, n) << 56
+    else:
+        keys = rng.integers(-2 ** 63, 2 ** 63 - 1, n, dtype=np.int64)
+    keys = np.asarray(keys, np.int64)
+    perm = impl.sfc_order(torch.from_numpy(keys).to(cuda)).cpu().numpy()
+    assert np.array_equal(perm, np.argsort(keys, kind="stable"))
+
+
+@pytest.mark.parametrize("n", [1, 1000, 300_001, 1_000_000, 2_200_001])
 def test_order_is_stable_argsort(cuda, n):
     print(f"\n[case] sfc order n={n}", flush=True)
     rng = np.random.default_rng(n)
