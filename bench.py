@@ -211,6 +211,49 @@ def main():
         graph_ms = ga.elapsed_time(gb) / args.steps
         del graph
 
+    # The rebuild preceded by the reference API's own SFC reorder of the atoms
+    # (sfc_kernels.cu:178-224: Morton keys, stable order) and the gather of the positions
+    # into that order, all on the device with no host sync, as one step: what a caller that
+    # applies the SFC permutation before every build pays.  (Positions frame 0.)
+    sfc_leg = None
+    if tgt is None and pos.dtype == torch.float32 and not args.vectors:
+        swsb = lib.dg_sfc_workspace_size(n)
+        sws = torch.empty(swsb, dtype=torch.uint8, device=dev)
+        keys = torch.empty(n, dtype=torch.int64, device=dev)
+        perm = torch.empty(n, dtype=torch.int64, device=dev)
+        ppos = torch.empty_like(pos)
+
+        def sfc_step():
+            L.check(lib.dg_sfc_keys(L.ptr(pos), n, 0, L.ptr(keys), L.ptr(sws), swsb, s), "sfc_keys")
+            L.check(lib.dg_sfc_order(L.ptr(keys), n, L.ptr(perm), L.ptr(sws), swsb, s), "sfc_order")
+            torch.index_select(pos, 0, perm, out=ppos)
+            L.check(lib.dg_graph_count(d, L.ptr(ppos), None, L.ptr(ws), wsb, L.ptr(counts), s), "count")
+            L.check(lib.dg_graph_write(d, L.ptr(ppos), None, L.ptr(ws), wsb, cap, L.ptr(src), L.ptr(dst),
+                                       L.ptr(shift), None, None, 0, s), "write")
+
+        for _ in range(max(2, args.warmup)):
+            sfc_step()
+        torch.cuda.synchronize()
+        sa, sb = torch.cuda.Event(enable_timing=True), torch.cuda.Event(enable_timing=True)
+        sa.record(stream)
+        for _ in range(args.steps):
+            sfc_step()
+        sb.record(stream)
+        torch.cuda.synchronize()
+        sfc_ms = sa.elapsed_time(sb) / args.steps
+        Ep = L._i64(0)
+        L.check(lib.dg_graph_read_totals(d, L.ptr(ws), Ep, fl, s), "totals")
+        Ep = int(Ep.value)
+        # + keys (read positions 12, write 8), order (read keys 8, write the permutation 8),
+        # gather (read the permutation 8 and positions 12, write positions 12): 68 B per atom
+        sfc_bytes = (12 * n + 16 * n + 24 * n + WRITE_BYTES_PER_EDGE * Ep) + 68 * n
+        sfc_leg = {"ms_per_rebuild": round(sfc_ms, 4), "value": round(Ep / (sfc_ms * 1e-3) / 1e9, 3),
+                   "unit": "Gedges/s", "edges": Ep, "algorithmic_bytes": sfc_bytes,
+                   "hbm_frac": round(sfc_bytes / (sfc_ms * 1e-3) / (HBM_PEAK_GBS * 1e9), 4),
+                   "steps": "dg_sfc_keys (Morton) + dg_sfc_order + gather of the positions + "
+                            "dg_graph_count + dg_graph_write on the permuted positions"}
+        del sws, keys, perm, ppos
+
     # drop-in Python API (exact-size outputs, one host sync per build)
 
     cell_t = torch.from_numpy(np.asarray(box.cell))
@@ -283,6 +326,7 @@ def main():
         "write_ms": round(write_ms, 4),
         "api_ms_per_rebuild": round(api_ms, 3),
         "graph_replay_ms_per_rebuild": None if graph_ms is None else round(graph_ms, 4),
+        "sfc_permuted_rebuild": sfc_leg,
         "roofline": {"bound": "hbm", "achieved": round(achieved, 1), "peak": HBM_PEAK_GBS,
                      "unit": "GB/s", "frac": round(achieved / HBM_PEAK_GBS, 4), "traffic": traffic,
                      "traffic_over_algorithmic": round(traffic / kbytes, 3) if traffic else None,
