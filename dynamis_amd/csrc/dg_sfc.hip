@@ -162,7 +162,10 @@ __global__ void keys_kernel(const float* __restrict__ pos, int64_t n, int curve,
 //                        pass, the int64 permutation.
 // Keys are kept with the sign bit flipped inside the sort (so they order as unsigned).
 constexpr int kRsBlock = 256;
-constexpr int kRsPer = 16;                     // keys per thread
+// 8 keys per thread (2048-key tiles, about two workgroups per CU at 1M keys): 1M Morton
+// keys in 0.205 ms, against 0.216 ms at 4, 0.208 ms at 6 and 0.246 ms at 16 keys per thread
+// (the scatter is latency-bound; smaller tiles put more of them in flight)
+constexpr int kRsPer = 8;                      // keys per thread
 constexpr int kRsTile = kRsBlock * kRsPer;     // keys per tile
 constexpr int kRsWaveKeys = 64 * kRsPer;       // a wave's contiguous share of a tile
 constexpr int kRsPasses = 8;
