@@ -90,3 +90,34 @@ def test_hilbert_keys_exhaustive_grid(cuda):
     k = impl.sfc_keys(torch.from_numpy(pos).to(cuda), 1).cpu().numpy()
     assert np.array_equal(k[:-2], sfc_twin.hilbert_from_grid(X, Y, Z))
     assert np.array_equal(k, oracle.hilbert_keys(pos))
+
+
+@pytest.mark.parametrize("name", ["C2-like 60k fp32", "C4 triclinic fp64"])
+def test_build_after_sfc_permutation(cuda, name):
+    """The reference API's SFC reorder followed by the build (what bench.py's
+    sfc_permuted_rebuild times): Morton keys, stable order, positions gathered into that
+    order on the device, then radius_graph_pbc_ex.  Mapped back through the permutation,
+    the edge set and the per-atom degrees must be the build's on the original order."""
+    from dynamis_amd import configs
+
+    box = configs.uniform(60_000, seed=71, dtype=np.float32) if name.startswith("C2") else configs.c4(scale=0.6)
+    print(f"\n[case] build after sfc permutation {name} N={len(box.pos)}", flush=True)
+    pos = torch.from_numpy(box.pos).to(cuda)
+    cell = torch.from_numpy(np.asarray(box.cell, np.float64))
+    pbc = torch.tensor(list(box.pbc))
+    keys = impl.sfc_keys(pos.float(), 0)
+    perm = impl.sfc_order(keys)
+    assert np.array_equal(perm.cpu().numpy(), np.argsort(keys.cpu().numpy(), kind="stable"))
+    ppos = torch.index_select(pos, 0, perm)
+    e0, s0, n0, c0 = impl.radius_graph_pbc_ex(pos, cell, pbc, box.radius, 0, False)
+    e1, s1, n1, c1 = impl.radius_graph_pbc_ex(ppos, cell, pbc, box.radius, 0, False)
+    p = perm.cpu().numpy()
+    assert int(n0.item()) == int(n1.item()) > 0
+    # degrees: atom p[i] of the original is atom i of the permuted build
+    deg = np.empty(len(p), np.int32)
+    deg[p] = c1.cpu().numpy()
+    assert np.array_equal(deg, c0.cpu().numpy())
+    got = oracle.canonical_sort(p[e1[0].cpu().numpy()], p[e1[1].cpu().numpy()], s1.cpu().numpy().astype(np.int64))
+    want = oracle.canonical_sort(e0[0].cpu().numpy(), e0[1].cpu().numpy(), s0.cpu().numpy().astype(np.int64))
+    for a, b in zip(got, want):
+        assert np.array_equal(a, b)
