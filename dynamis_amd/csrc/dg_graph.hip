@@ -2512,13 +2512,17 @@ static void* g_scratch_ptr[kMaxDevices];
 // Overlap guard, per device: the stream of the last call and an event recorded behind it.
 // A call on another stream while that event is still pending would share the scratch with
 // work in flight, and is refused.  (Created once per device, with the scratch lookup.)
+// A call holds its device's array (busy) from the check until its work is enqueued, so two
+// host threads cannot both pass the check.
 static hipEvent_t g_scratch_done[kMaxDevices];
 static hipStream_t g_scratch_stream[kMaxDevices];
 static bool g_scratch_used[kMaxDevices];
+static bool g_scratch_busy[kMaxDevices];
 
-// The scratch address on the current device, looked up once per device.
+// The scratch address on the current device, looked up once per device, and the device's
+// array taken for this call (*dev_out; give it back with scratch_release).
 // The stream must belong to the current device: the address is that device's copy.
-static dg_status scratch_on_current_device(hipStream_t s, void** out)
+static dg_status scratch_on_current_device(hipStream_t s, void** out, int* dev_out)
 {
     int dev = -1;
     hipError_t e = hipGetDevice(&dev);
@@ -2549,6 +2553,9 @@ static dg_status scratch_on_current_device(hipStream_t s, void** out)
         e = hipStreamIsCapturing(s, &cap);
         if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipStreamIsCapturing: ") + hipGetErrorString(e));
     }
+    if (g_scratch_busy[dev])
+        return fail(DG_ERR_INVALID, "dg_graph_build_noalloc: another call on this device is being enqueued "
+                                    "(calls share the static scratch and must not overlap)");
     if (cap == hipStreamCaptureStatusNone && g_scratch_used[dev] && g_scratch_stream[dev] != s) {
         e = hipEventQuery(g_scratch_done[dev]);
         if (e == hipErrorNotReady)
@@ -2557,21 +2564,22 @@ static dg_status scratch_on_current_device(hipStream_t s, void** out)
                                         "scratch and must not overlap");
         if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipEventQuery: ") + hipGetErrorString(e));
     }
+    g_scratch_busy[dev] = true;
     *out = g_scratch_ptr[dev];
+    *dev_out = dev;
     return DG_OK;
 }
 
-// Marks the end of a call on stream s (current device): the overlap guard's event.
-static dg_status scratch_release(hipStream_t s)
+// Gives back device dev's array after a call on stream s: records the overlap guard's event
+// behind whatever the call enqueued (not on a stream under capture).
+static dg_status scratch_release(int dev, hipStream_t s)
 {
-    int dev = -1;
-    hipError_t e = hipGetDevice(&dev);
-    if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipGetDevice: ") + hipGetErrorString(e));
     hipStreamCaptureStatus cap = hipStreamCaptureStatusNone;
     if (s != nullptr && hipStreamIsCapturing(s, &cap) != hipSuccess) cap = hipStreamCaptureStatusActive;
-    if (cap != hipStreamCaptureStatusNone) return DG_OK;
     std::lock_guard<std::mutex> lock(g_scratch_mu);
-    e = hipEventRecord(g_scratch_done[dev], s);
+    g_scratch_busy[dev] = false;
+    if (cap != hipStreamCaptureStatusNone) return DG_OK;
+    const hipError_t e = hipEventRecord(g_scratch_done[dev], s);
     if (e != hipSuccess) return fail(DG_ERR_HIP, std::string("hipEventRecord: ") + hipGetErrorString(e));
     g_scratch_stream[dev] = s;
     g_scratch_used[dev] = true;
@@ -2602,15 +2610,23 @@ extern "C" dg_status dg_graph_build_noalloc(const dg_graph_desc* desc, const voi
                                           "scratch holds " + std::to_string(kScratchBytes) +
                                           " (use dg_graph_build with a caller workspace)");
     void* ws = nullptr;
-    st = scratch_on_current_device(s, &ws);
+    int dev = -1;
+    st = scratch_on_current_device(s, &ws, &dev);
     if (st != DG_OK) return st;
     st = dg_graph_build(desc, pos, target_idx, ws, kScratchBytes, capacity, counts_out, edge_src,
                         edge_dst, cell_shift, edge_vec, edge_dist, vec_dtype, s);
-    if (st != DG_OK) return st;
-    hipLaunchKernelGGL(copy_totals_kernel, dim3(1), dim3(64), 0, s,
-                       (const int64_t*)at<int64_t>(ws, p.o_tot), totals_out);
-    st = check_launch("dg_graph_build_noalloc");
-    if (st != DG_OK) return st;
-    return scratch_release(s);
+    if (st == DG_OK) {
+        hipLaunchKernelGGL(copy_totals_kernel, dim3(1), dim3(64), 0, s,
+                           (const int64_t*)at<int64_t>(ws, p.o_tot), totals_out);
+        st = check_launch("dg_graph_build_noalloc");
+    }
+    // (also after a failed call: whatever it enqueued still uses the array)
+    const std::string err = st != DG_OK ? g_last_error : std::string();
+    const dg_status rs = scratch_release(dev, s);
+    if (st != DG_OK) {
+        g_last_error = err;
+        return st;
+    }
+    return rs;
 }
 #endif  // DG_MAIN_TU

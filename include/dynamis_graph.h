@@ -152,9 +152,10 @@ dg_status dg_graph_build(const dg_graph_desc* desc, const void* pos, const int64
  * DG_FLAG_CAPACITY, means the tiles that did not fit were skipped).  Every call on one
  * GPU shares that GPU's array: calls that overlap on one GPU race.  Calls on one stream
  * are ordered by it; a call on another stream while the previous call's work is still
- * pending on the GPU is refused with DG_ERR_INVALID (a host-side check of an event the
- * library records behind every call; calls on a stream under graph capture are not
- * checked, and ordering such calls is the caller's part).  The stream must belong to the
+ * pending on the GPU, or while another host thread is enqueueing a call on the same GPU,
+ * is refused with DG_ERR_INVALID (a host-side check of an event the library records
+ * behind every call; calls on a stream under graph capture are not checked, and ordering
+ * such calls is the caller's part).  The stream must belong to the
  * current device (DG_ERR_INVALID otherwise). */
 dg_status dg_graph_build_noalloc(const dg_graph_desc* desc, const void* pos,
                                  const int64_t* target_idx, int64_t capacity, int32_t* counts_out,
