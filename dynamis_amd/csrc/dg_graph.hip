@@ -292,7 +292,8 @@ __global__ void order_atoms_kernel(int64_t n, const uint32_t* __restrict__ key,
 // per-bin counting sort): kSortChunks workgroups each histogram the tiles of one chunk of
 // atoms in LDS and reserve their share of every tile with one device atomic per tile;
 // the same chunks then place their atoms into tile buckets; one workgroup per tile then
-// orders its bucket by (bin, atom id) in LDS and writes the bin starts and the cell list.
+// orders its bucket by (bin, x in the bin, atom id) in LDS and writes the bin starts and the
+// cell list.
 
 // Chunk c of the atoms: [c n / G, (c + 1) n / G).
 __device__ __forceinline__ void sort_chunk(int64_t n, int64_t* lo, int64_t* hi)
@@ -393,6 +394,7 @@ struct TileSortLds {
         int by[kTileSortCap];  // ids grouped by bin
         SegSortLds seg;        // a larger bucket: sorted in global memory
     };
+    uint32_t bx[kTileSortCap];  // atoms: order key of each grouped entry's x in its bin
     int cnt[kTileMax * kTileMax * kTileMax];
     int st[kTileMax * kTileMax * kTileMax + 1];
     int w32[4];
@@ -414,11 +416,24 @@ struct TileSortOut {
     int* tsidx;
     const int64_t* run_if;  // targets: skipped when *run_if == 0 (they need no sort)
     void* stmp;             // scratch for a bucket of more than kTileSortCap entries (one per entry)
+    int64_t* xflag;         // atoms: raised when a bucket's bins are left in id order
+    int xorder;             // atoms: order bins by (x, id) (else by id)
 };
 
-// One workgroup per tile: orders its bucket by (bin, id), writes the tile's bin starts and
-// its part of the sorted list.  Each entry's payload is gathered into registers as soon as
-// its id is known, so the gathers overlap the ordering in LDS.
+// Order key of a float: unsigned compare of the keys is the float order (-0 below +0).
+__device__ __forceinline__ uint32_t float_order_key(float x)
+{
+    const uint32_t u = __float_as_uint(x);
+    return u ^ ((uint32_t)((int32_t)u >> 31) | 0x80000000u);
+}
+
+// One workgroup per tile: orders its bucket by bin, writes the tile's bin starts and its
+// part of the sorted list.  Inside a bin, atoms go by (x relative to the bin origin, id),
+// so that the count pass can cut a stencil row's end bins at quarter-bin x boundaries;
+// explicit targets go by caller position.  A bucket too large for LDS is ordered by (bin,
+// id) and raises *xflag (the count pass then uses whole bins).  Each entry's payload is
+// gathered into registers as soon as its id is known, so the gathers overlap the ordering
+// in LDS.
 template <bool TGT, typename BT>
 __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64_t ntiles,
                                                         const int* __restrict__ tstart,
@@ -489,6 +504,9 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
     if (!fits) {
         // a very dense tile: the bucket sorted by (bin, id) in global memory (an entry's
         // bin sits above its id), then each entry goes to its place
+        if constexpr (!TGT)
+            if (o.xorder && threadIdx.x == 0 && flag_clear(o.xflag))
+                atomicOr((unsigned long long*)o.xflag, 1ull);
         segment_sort<BT>(bucket + base, (BT*)o.stmp + base, m, sizeof(BT) == 4 ? 32 : 40, S.seg);
         for (int e = threadIdx.x; e < m; e += 256) {
             const int i = bk_id(bucket[base + e]);
@@ -496,17 +514,30 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
         }
         return;
     }
+    uint32_t qx[kTileSortPer];
 #pragma unroll
-    for (int u = 0; u < kTileSortPer; ++u)
-        if (qi[u] >= 0) S.by[atomicAdd(&S.cnt[ql[u]], 1)] = qi[u];
+    for (int u = 0; u < kTileSortPer; ++u) {
+        if constexpr (TGT) qx[u] = 0;
+        else qx[u] = o.xorder ? float_order_key(q[u].x) : 0u;
+        if (qi[u] >= 0) {
+            const int d = atomicAdd(&S.cnt[ql[u]], 1);
+            S.by[d] = qi[u];
+            S.bx[d] = qx[u];
+        }
+    }
     __syncthreads();
-    // each entry's place in its bin: the number of smaller ids there
+    // each entry's place in its bin: the number of entries there with a smaller (x, id)
+    // (targets, and atoms without xorder: x keys all 0, so by id)
 #pragma unroll
     for (int u = 0; u < kTileSortPer; ++u) {
         if (qi[u] < 0) continue;
         const int i = qi[u], l = ql[u];
+        const uint32_t x = qx[u];
         int below = 0;
-        for (int k = S.st[l]; k < S.st[l + 1]; ++k) below += S.by[k] < i;
+        for (int k = S.st[l]; k < S.st[l + 1]; ++k) {
+            const uint32_t xk = S.bx[k];
+            below += (xk < x) | ((xk == x) & (S.by[k] < i));
+        }
         emit(base + S.st[l] + below, i, q[u]);
     }
 }
@@ -652,6 +683,7 @@ struct SearchArgs {
     uint16_t* slot;
     int K;
     int64_t nslot;  // targets (group row length)
+    int xsplit;     // bins ordered by x unless *xflag (see tile_sort_kernel): quarter-bin row ends
 };
 
 // Whether this build's targets are the atoms of the tile with ids < ntarg (see SearchArgs).
@@ -1289,7 +1321,9 @@ struct TileOut {
     int g0[3];
 };
 
-template <int MODE>
+// QS (count pass, orthorhombic cells, cell list ordered by x inside bins): the quarter-bin
+// row ends described below; false: whole bins, any cell.
+template <int MODE, bool QS = false>
 __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                                                typename LdsOf<MODE>::type& sh, int64_t ord)
 {
@@ -1365,6 +1399,17 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
     }
     __syncthreads();
     const int nchunks = (total + kCap - 1) / kCap;
+    // Quarter-bin row ends (QS: count pass, orthorhombic cell; a one-chunk region whose bins
+    // are ordered by x): staging packs into each rp word, above its 20-bit first entry, the
+    // number of the bin's entries whose x offset in the bin lies below each of its x
+    // quarter boundaries (3 x 4 bits; 15: 15 or more), and a row then starts at the quarter
+    // of its first bin that the cutoff reaches and ends after the quarter of its last.
+    // Entries cut off this way lie beyond the padded cutoff along x alone, so they are never
+    // edges: every target's edge sequence is unchanged (the fix-up pass, which sweeps whole
+    // bins, numbers edges alike).
+    const bool qsplit = QS && nchunks == 1 && a.totals[4] == 0;
+    const int rpm = qsplit ? 0xFFFFF : -1;  // first-entry bits of an rp word
+    const float qb1 = 0.25f * a.hax, qb2 = 0.5f * a.hax, qb3 = 0.75f * a.hax;
     // slots hold up to two chunks' entries (2-byte byte offsets in the region); a larger
     // region is written directly by search_kernel<1>
     // (the write pass follows what the count pass recorded: a tile it flagged as chunked --
@@ -1397,6 +1442,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             float o[3];
             region_offset(a, r[0], r[1], r[2], o);
             const int g = rst[h] - rex[h];  // cell-list index minus region index
+            int s1 = 0, s2 = 0, s3 = 0;  // entries below the quarter boundaries
             for (int vv = b0; vv < b1; vv += 4) {
                 float4 e[4];
 #pragma unroll
@@ -1407,8 +1453,15 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                     if (vv + u < b1) {
                         shq[vv + u - c0] = make_float4(e[u].x + o[0], e[u].y + o[1], e[u].z + o[2], e[u].w);
                         if constexpr (WRITE) sh.T[vv + u - c0] = entry_T(rb, g + vv + u);
+                        if constexpr (QS) {
+                            s1 += e[u].x < qb1;
+                            s2 += e[u].x < qb2;
+                            s3 += e[u].x < qb3;
+                        }
                     }
             }
+            if (QS && qsplit)  // (one chunk: [b0, b1) is the whole bin)
+                sh.rp[rb] = rex[h] | (int)((uint32_t)(min(s1, 15) | (min(s2, 15) << 4) | (min(s3, 15) << 8)) << 20);
         }
     };
     auto ensure_chunk = [&](int c) {  // uniform
@@ -1457,7 +1510,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             // the target's own region entry (same atom, zero shift) is never an edge
             const int rb_self = ((lz + a.P[2]) * R1 + (ly + a.P[1])) * R0 + (lx + a.P[0]);
             const int bin_start = listed ? a.bstart[kb + lo] : sh.tbs[lo];
-            v_self = sh.rp[rb_self] + (sidx - bin_start);
+            v_self = (sh.rp[rb_self] & rpm) + (sidx - bin_start);
         }
         const int fx = unpack3(my_f, 0), fy = unpack3(my_f, 1), fz = unpack3(my_f, 2);
         // the target's position inside its bin in bin units (lower-triangular cells)
@@ -1466,6 +1519,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         const float Oz = uz * a.inv_hcz, Oy = (uy - Oz * a.hcy) * a.inv_hby,
                     Ox = (ux - Oy * a.hbx - Oz * a.hcx) * a.inv_hax;
         const float Oxp = Ox + (float)a.P[0];  // (orthorhombic rows: x bins from the region's first)
+        const float Oxp4 = 4.f * Oxp, inv_hax4 = 4.f * a.inv_hax;  // in quarter bins (exact scalings)
 
         // Sweep this lane's target over the resident chunk c, in the fixed order (dz, dy,
         // x, atom) -- ascending region index; on_cand(v, edge, k) receives every candidate's
@@ -1483,8 +1537,9 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         auto row_range = [&](int ri, int c0, int c1, int& va, int& vb) {
             const int oz = ri / nry, oy = ri - oz * nry;
             int xlo = 0, xhi = nrx - 1;
+            int qlo = 0, qhi = 3;  // first and last quarter of the end bins
             va = vb = 0;
-            if (a.lowtri == 2) {
+            if (QS || a.lowtri == 2) {
                 // orthorhombic: the row's bins span y in [py, py + 1] hby and z in
                 // [pz, pz + 1] hcz around the target; their gaps (less the margin) bound the
                 // distance from below, and the x range follows without shear
@@ -1494,9 +1549,22 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 const float rem2 = fmaf(-gz, gz, fmaf(-gy, gy, a.rprune2));
                 if (rem2 < 0.f) return;
                 const float rem = __builtin_amdgcn_sqrtf(rem2);
-                xlo = max((int)floorf(fmaf(-rem, a.inv_hax, Oxp)), 0);
-                xhi = min((int)floorf(fmaf(rem, a.inv_hax, Oxp)), nrx - 1);
-                if (xlo > xhi) return;
+                if constexpr (QS) {
+                    // (4 floor(u) + quarter = floor(4 u): the bins are those of floor(u))
+                    const int QL = max((int)floorf(fmaf(-rem, inv_hax4, Oxp4)), 0);
+                    const int QH = min((int)floorf(fmaf(rem, inv_hax4, Oxp4)), 4 * nrx - 1);
+                    xlo = QL >> 2;
+                    xhi = QH >> 2;
+                    if (xlo > xhi) return;
+                    if (qsplit) {
+                        qlo = QL & 3;
+                        qhi = QH & 3;
+                    }
+                } else {
+                    xlo = max((int)floorf(fmaf(-rem, a.inv_hax, Oxp)), 0);
+                    xhi = min((int)floorf(fmaf(rem, a.inv_hax, Oxp)), nrx - 1);
+                    if (xlo > xhi) return;
+                }
             } else if (a.lowtri) {
                 // bounding box of the row (bins py, pz relative to the target's bin, all x)
                 // in Cartesian y and z, from the target: its gaps gy, gz bound the distance
@@ -1520,8 +1588,18 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 if (xlo > xhi) return;
             }
             const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
-            va = max(sh.rp[rb + xlo], c0) - c0;
-            vb = min(sh.rp[rb + xhi + 1], c1) - c0;
+            int sa, sb;
+            if (QS && qsplit) {  // (wave-uniform)
+                const uint32_t wl = (uint32_t)sh.rp[rb + xlo], wh = (uint32_t)sh.rp[rb + xhi];
+                sa = (int)(wl & 0xFFFFFu) + (int)((wl >> (16 + 4 * qlo)) & (qlo ? 15u : 0u));
+                const int ch = (int)((wh >> (20 + 4 * min(qhi, 2))) & 15u);
+                sb = qhi < 3 && ch != 15 ? (int)(wh & 0xFFFFFu) + ch : (sh.rp[rb + xhi + 1] & 0xFFFFF);
+            } else {
+                sa = sh.rp[rb + xlo];
+                sb = sh.rp[rb + xhi + 1];
+            }
+            va = max(sa, c0) - c0;
+            vb = min(sb, c1) - c0;
             if (va >= vb) va = vb = 0;
             va <<= 4;  // byte offsets of the 16-byte entries
             vb <<= 4;
@@ -1763,12 +1841,13 @@ __device__ __forceinline__ void expand_one(const SearchArgs& a, typename ExpandL
 
 // MODE 0 (count) and MODE 1 (fix-up write): one tile per workgroup.  The fix-up also
 // expands the slots of the two-chunk tiles (their region needs the larger staging buffer).
-template <int MODE>
+// QS: the count with quarter-bin row ends (orthorhombic cells, cell list ordered by x).
+template <int MODE, bool QS = false>
 __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 {
     if constexpr (MODE == 0) {
         __shared__ CountLds sh;
-        search_tile<0>(a, sh, blockIdx.x);
+        search_tile<0, QS>(a, sh, blockIdx.x);
     } else {
         __shared__ union {
             FixLds f;
@@ -2043,6 +2122,16 @@ dg_status make_plan(const dg_graph_desc* d, Plan& p)
     return DG_OK;
 }
 
+// 2: orthorhombic cell; 1: other lower-triangular cell (a along x, b in the xy plane,
+// positive diagonal); 0: any other.
+int cell_shape(const Plan& p)
+{
+    const bool low = p.C[1] == 0.0 && p.C[2] == 0.0 && p.C[5] == 0.0 && p.C[0] > 0.0 && p.C[4] > 0.0 &&
+                     p.C[8] > 0.0;
+    if (!low) return 0;
+    return p.C[3] == 0.0 && p.C[6] == 0.0 && p.C[7] == 0.0 ? 2 : 1;
+}
+
 GridArgs grid_args(const Plan& p)
 {
     GridArgs g;
@@ -2064,8 +2153,7 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     for (int d = 0; d < 3; ++d)
         for (int c = 0; c < 3; ++c) a.hC[3 * d + c] = p.C[3 * d + c] / (double)p.nb[d];
     a.r2 = p.r2;
-    a.lowtri = p.C[1] == 0.0 && p.C[2] == 0.0 && p.C[5] == 0.0 && p.C[0] > 0.0 && p.C[4] > 0.0 &&
-               p.C[8] > 0.0;
+    a.lowtri = cell_shape(p);
     a.hax = (float)(p.C[0] / p.nb[0]);
     a.hbx = (float)(p.C[3] / p.nb[1]);
     a.hby = (float)(p.C[4] / p.nb[1]);
@@ -2079,7 +2167,6 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     // cutoff by far more than the fp32 position error
     a.pmargin = (float)(1e-4 * p.r + 1e-3);
     a.rprune2 = (float)((p.r + 2.0 * a.pmargin) * (p.r + 2.0 * a.pmargin));
-    if (a.lowtri && p.C[3] == 0.0 && p.C[6] == 0.0 && p.C[7] == 0.0) a.lowtri = 2;
     a.gy_off = -a.hby - a.pmargin;
     a.gz_off = -a.hcz - a.pmargin;
     for (int d = 0; d < 3; ++d) {
@@ -2088,6 +2175,7 @@ SearchArgs search_args(const Plan& p, const void* pos, void* ws)
     }
     a.tb = p.tb;
     a.nregion = p.nregion;
+    a.xsplit = p.ntiles <= kSortTilesMax;  // (the per-bin sort above keeps bins in id order)
     a.ntiles = p.ntiles;
     a.toff = p.toff; a.hi_off = p.hi_off; a.lo_bits = p.lo_bits;
     a.spos = at<float4>(ws, p.o_spos);
@@ -2206,6 +2294,8 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         o.sid = at<int>(ws, p.o_sid);
         o.inv = p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr;
         o.stmp = at<void>(ws, p.o_stmp);
+        o.xflag = totals + 4;
+        o.xorder = cell_shape(p) == 2;  // (only the orthorhombic count cuts bins by x)
         if (narrow)
             hipLaunchKernelGGL((tile_sort_kernel<false, uint32_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n,
                                p.tb, p.ntiles, (const int*)tstart, at<uint32_t>(ws, p.o_arr), bstart, o);
@@ -2298,7 +2388,10 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
 #else   // DG_COUNT_TU
 void launch_count_kernel(const SearchArgs& a, unsigned grid, hipStream_t s)
 {
-    hipLaunchKernelGGL(search_kernel<0>, dim3(grid), dim3(kBlock), 0, s, a);
+    if (a.lowtri == 2 && a.xsplit)
+        hipLaunchKernelGGL((search_kernel<0, true>), dim3(grid), dim3(kBlock), 0, s, a);
+    else
+        hipLaunchKernelGGL((search_kernel<0, false>), dim3(grid), dim3(kBlock), 0, s, a);
 }
 #endif  // DG_MAIN_TU
 

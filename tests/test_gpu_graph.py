@@ -495,6 +495,36 @@ def test_near_cutoff_pairs(cuda, dtype, shape):
 
 
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
+@pytest.mark.parametrize("shape", ["cubic", "lowtri"])
+def test_near_cutoff_pairs_along_x(cuda, dtype, shape):
+    """Pairs within a few ulp of the cutoff, mostly along x, in a background at C3's density
+    (0.1 per cubic angstrom, so bins hold a few atoms each).  The count pass starts and ends
+    each stencil row at quarter-bin x boundaries of its end bins (bins ordered by x): every
+    partner here sits near the far x end of some anchor's rows, where a cut one quarter too
+    deep would drop it."""
+    cell = {"cubic": np.eye(3) * 48.0,
+            "lowtri": np.array([[48.0, 0, 0], [12.0, 46.0, 0], [-8.0, 10.0, 45.0]])}[shape]
+    r = 6.0
+    rng = np.random.default_rng(31)
+    vol = abs(np.linalg.det(cell))
+    bg = rng.uniform(0, 1, (int(0.1 * vol), 3)) @ cell
+    anchors = rng.uniform(0, 1, (600, 3)) @ cell
+    eps = np.array([-3e-6, -1e-6, -1e-7, 0.0, 1e-7, 1e-6, 3e-6])
+    n_e = len(eps)
+    # y, z offsets up to 3 A (the rows of the anchor's bin and its neighbours), x from the
+    # distance; both x directions
+    yz = rng.uniform(-3.0, 3.0, (len(anchors), n_e, 2))
+    dist = r * (1.0 + eps)[None, :]
+    dx = np.sqrt(dist ** 2 - (yz ** 2).sum(-1))
+    sgn = np.where(rng.uniform(size=dx.shape) < 0.5, -1.0, 1.0)
+    off = np.concatenate([(sgn * dx)[..., None], yz], axis=-1)
+    partners = anchors[:, None, :] + off
+    pos = np.concatenate([bg, anchors, partners.reshape(-1, 3)]).astype(dtype)
+    _, _, cnt, o = check_parity(pos, cell, (1, 1, 1), r, cuda, name=f"near-cutoff along x {shape}")
+    assert len(o["src"]) > 0.1 * vol * 30
+
+
+@pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("shape", ["cubic", "general"])
 def test_near_coincident_atoms(cuda, dtype, shape):
     """Distinct atoms at or near the same place: exact duplicates (d2 = 0, never an edge)
