@@ -1590,10 +1590,12 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
             int sa, sb;
             if (QS && qsplit) {  // (wave-uniform)
-                const uint32_t wl = (uint32_t)sh.rp[rb + xlo], wh = (uint32_t)sh.rp[rb + xhi];
+                // (all three words read unconditionally: a select, not a branch)
+                const uint32_t wl = (uint32_t)sh.rp[rb + xlo], wh = (uint32_t)sh.rp[rb + xhi],
+                               we = (uint32_t)sh.rp[rb + xhi + 1];
                 sa = (int)(wl & 0xFFFFFu) + (int)((wl >> (16 + 4 * qlo)) & (qlo ? 15u : 0u));
                 const int ch = (int)((wh >> (20 + 4 * min(qhi, 2))) & 15u);
-                sb = qhi < 3 && ch != 15 ? (int)(wh & 0xFFFFFu) + ch : (sh.rp[rb + xhi + 1] & 0xFFFFF);
+                sb = (int)((qhi < 3 && ch != 15 ? wh + (uint32_t)ch : we) & 0xFFFFFu);
             } else {
                 sa = sh.rp[rb + xlo];
                 sb = sh.rp[rb + xhi + 1];
