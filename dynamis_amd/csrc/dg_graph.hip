@@ -103,6 +103,21 @@ struct GridArgs {
     int tb;
 };
 
+// Offset of a cell-list record along the cell's a axis inside its bin, as a Cartesian x
+// length (lower-triangular cells): x less the b and c shears of its y and z offsets, so the
+// key is fa * hax for the record's fraction fa of the bin along a.  The tile sort orders
+// bins by it and the count pass counts quarter-bin prefixes of it: both evaluate it with
+// these explicit operations on the same inputs, so the counts are prefixes of the order.
+struct XKey {
+    float hbx, hcx, hcy, inv_hby, inv_hcz;
+};
+__device__ __forceinline__ float bin_xkey(const float4& e, const XKey& k)
+{
+    const float fc = e.z * k.inv_hcz;
+    const float fb = fmaf(-fc, k.hcy, e.y) * k.inv_hby;
+    return fmaf(-fc, k.hcx, fmaf(-fb, k.hbx, e.x));
+}
+
 #if DG_MAIN_TU
 // ---------------------------------------------------------------- tile SFC ranks
 // Rank of every tile in the compact Morton order (morton_encode) among the tiles of the
@@ -417,7 +432,8 @@ struct TileSortOut {
     const int64_t* run_if;  // targets: skipped when *run_if == 0 (they need no sort)
     void* stmp;             // scratch for a bucket of more than kTileSortCap entries (one per entry)
     int64_t* xflag;         // atoms: raised when a bucket's bins are left in id order
-    int xorder;             // atoms: order bins by (x, id) (else by id)
+    int xorder;             // atoms: order bins by (bin_xkey, id) (else by id)
+    XKey xk;
 };
 
 // Order key of a float: unsigned compare of the keys is the float order (-0 below +0).
@@ -518,7 +534,7 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
 #pragma unroll
     for (int u = 0; u < kTileSortPer; ++u) {
         if constexpr (TGT) qx[u] = 0;
-        else qx[u] = o.xorder ? float_order_key(q[u].x) : 0u;
+        else qx[u] = o.xorder ? float_order_key(bin_xkey(q[u], o.xk)) : 0u;
         if (qi[u] >= 0) {
             const int d = atomicAdd(&S.cnt[ql[u]], 1);
             S.by[d] = qi[u];
@@ -1321,9 +1337,10 @@ struct TileOut {
     int g0[3];
 };
 
-// QS (count pass, orthorhombic cells, cell list ordered by x inside bins): the quarter-bin
-// row ends described below; false: whole bins, any cell.
-template <int MODE, bool QS = false>
+// QS (count pass, cell list ordered by bin_xkey inside bins): the quarter-bin row ends
+// described below, for orthorhombic (1) or other lower-triangular cells (2); 0: whole
+// bins, any cell.
+template <int MODE, int QS = 0>
 __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                                                typename LdsOf<MODE>::type& sh, int64_t ord)
 {
@@ -1399,15 +1416,17 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
     }
     __syncthreads();
     const int nchunks = (total + kCap - 1) / kCap;
-    // Quarter-bin row ends (QS: count pass, orthorhombic cell; a one-chunk region whose bins
-    // are ordered by x): staging packs into each rp word, above its 20-bit first entry, the
-    // number of the bin's entries whose x offset in the bin lies below each of its x
-    // quarter boundaries (3 x 4 bits; 15: 15 or more), and a row then starts at the quarter
-    // of its first bin that the cutoff reaches and ends after the quarter of its last.
+    // Quarter-bin row ends (QS: count pass, lower-triangular cell; a one-chunk region whose
+    // bins are ordered by bin_xkey): staging packs into each rp word, above its 20-bit first
+    // entry, the number of the bin's entries whose key lies below each of its quarter
+    // boundaries (3 x 4 bits; 15: 15 or more), and a row then starts at the quarter of its
+    // first bin that the cutoff reaches and ends after the quarter of its last.
     // Entries cut off this way lie beyond the padded cutoff along x alone, so they are never
     // edges: every target's edge sequence is unchanged (the fix-up pass, which sweeps whole
     // bins, numbers edges alike).
-    const bool qsplit = QS && nchunks == 1 && a.totals[4] == 0;
+    const bool qsplit = QS != 0 && nchunks == 1 && a.totals[4] == 0;
+    XKey xkey;
+    xkey.hbx = a.hbx; xkey.hcx = a.hcx; xkey.hcy = a.hcy; xkey.inv_hby = a.inv_hby; xkey.inv_hcz = a.inv_hcz;
     const int rpm = qsplit ? 0xFFFFF : -1;  // first-entry bits of an rp word
     const float qb1 = 0.25f * a.hax, qb2 = 0.5f * a.hax, qb3 = 0.75f * a.hax;
     // slots hold up to two chunks' entries (2-byte byte offsets in the region); a larger
@@ -1453,14 +1472,15 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                     if (vv + u < b1) {
                         shq[vv + u - c0] = make_float4(e[u].x + o[0], e[u].y + o[1], e[u].z + o[2], e[u].w);
                         if constexpr (WRITE) sh.T[vv + u - c0] = entry_T(rb, g + vv + u);
-                        if constexpr (QS) {
-                            s1 += e[u].x < qb1;
-                            s2 += e[u].x < qb2;
-                            s3 += e[u].x < qb3;
+                        if constexpr (QS != 0) {
+                            const float xk = QS == 1 ? e[u].x : bin_xkey(e[u], xkey);
+                            s1 += xk < qb1;
+                            s2 += xk < qb2;
+                            s3 += xk < qb3;
                         }
                     }
             }
-            if (QS && qsplit)  // (one chunk: [b0, b1) is the whole bin)
+            if (QS != 0 && qsplit)  // (one chunk: [b0, b1) is the whole bin)
                 sh.rp[rb] = rex[h] | (int)((uint32_t)(min(s1, 15) | (min(s2, 15) << 4) | (min(s3, 15) << 8)) << 20);
         }
     };
@@ -1539,7 +1559,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
             int xlo = 0, xhi = nrx - 1;
             int qlo = 0, qhi = 3;  // first and last quarter of the end bins
             va = vb = 0;
-            if (QS || a.lowtri == 2) {
+            if (QS == 1 || (QS == 0 && a.lowtri == 2)) {
                 // orthorhombic: the row's bins span y in [py, py + 1] hby and z in
                 // [pz, pz + 1] hcz around the target; their gaps (less the margin) bound the
                 // distance from below, and the x range follows without shear
@@ -1549,7 +1569,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 const float rem2 = fmaf(-gz, gz, fmaf(-gy, gy, a.rprune2));
                 if (rem2 < 0.f) return;
                 const float rem = __builtin_amdgcn_sqrtf(rem2);
-                if constexpr (QS) {
+                if constexpr (QS == 1) {
                     // (4 floor(u) + quarter = floor(4 u): the bins are those of floor(u))
                     const int QL = max((int)floorf(fmaf(-rem, inv_hax4, Oxp4)), 0);
                     const int QH = min((int)floorf(fmaf(rem, inv_hax4, Oxp4)), 4 * nrx - 1);
@@ -1565,7 +1585,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                     xhi = min((int)floorf(fmaf(rem, a.inv_hax, Oxp)), nrx - 1);
                     if (xlo > xhi) return;
                 }
-            } else if (a.lowtri) {
+            } else if (QS == 2 || (QS == 0 && a.lowtri)) {
                 // bounding box of the row (bins py, pz relative to the target's bin, all x)
                 // in Cartesian y and z, from the target: its gaps gy, gz bound the distance
                 // from below; the x range that the (padded) cutoff sphere can reach then
@@ -1583,13 +1603,29 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 const float rem = __builtin_amdgcn_sqrtf(rem2);
                 const float sl = fminf(py * a.hbx, (py + 1.f) * a.hbx) + fminf(pz * a.hcx, (pz + 1.f) * a.hcx);
                 const float sh = fmaxf(py * a.hbx, (py + 1.f) * a.hbx) + fmaxf(pz * a.hcx, (pz + 1.f) * a.hcx);
-                xlo = max((int)floorf(Ox + (-rem - sh) * a.inv_hax) + a.P[0], 0);
-                xhi = min((int)floorf(Ox + (rem - sl) * a.inv_hax) + a.P[0], nrx - 1);
-                if (xlo > xhi) return;
+                if constexpr (QS == 2) {
+                    // in quarter bins, as the orthorhombic rows: an entry of the first bin
+                    // whose a fraction is below u - xlo lies at least rem below the target
+                    // in x (its shear is at most sh), one of the last bin at or above
+                    // w - xhi at least rem above it (its shear is at least sl)
+                    const int QL = max((int)floorf(4.f * (Ox + (-rem - sh) * a.inv_hax)) + 4 * a.P[0], 0);
+                    const int QH = min((int)floorf(4.f * (Ox + (rem - sl) * a.inv_hax)) + 4 * a.P[0], 4 * nrx - 1);
+                    xlo = QL >> 2;
+                    xhi = QH >> 2;
+                    if (xlo > xhi) return;
+                    if (qsplit) {
+                        qlo = QL & 3;
+                        qhi = QH & 3;
+                    }
+                } else {
+                    xlo = max((int)floorf(Ox + (-rem - sh) * a.inv_hax) + a.P[0], 0);
+                    xhi = min((int)floorf(Ox + (rem - sl) * a.inv_hax) + a.P[0], nrx - 1);
+                    if (xlo > xhi) return;
+                }
             }
             const int rb = ((lz + oz) * R1 + (ly + oy)) * R0 + lx;
             int sa, sb;
-            if (QS && qsplit) {  // (wave-uniform)
+            if (QS != 0 && qsplit) {  // (wave-uniform)
                 // (all three words read unconditionally: a select, not a branch)
                 const uint32_t wl = (uint32_t)sh.rp[rb + xlo], wh = (uint32_t)sh.rp[rb + xhi],
                                we = (uint32_t)sh.rp[rb + xhi + 1];
@@ -1843,8 +1879,9 @@ __device__ __forceinline__ void expand_one(const SearchArgs& a, typename ExpandL
 
 // MODE 0 (count) and MODE 1 (fix-up write): one tile per workgroup.  The fix-up also
 // expands the slots of the two-chunk tiles (their region needs the larger staging buffer).
-// QS: the count with quarter-bin row ends (orthorhombic cells, cell list ordered by x).
-template <int MODE, bool QS = false>
+// QS: the count with quarter-bin row ends (1: orthorhombic cells, 2: other lower-triangular
+// cells; cell list ordered by bin_xkey).
+template <int MODE, int QS = 0>
 __global__ __launch_bounds__(kBlock) void search_kernel(SearchArgs a)
 {
     if constexpr (MODE == 0) {
@@ -2134,6 +2171,18 @@ int cell_shape(const Plan& p)
     return p.C[3] == 0.0 && p.C[6] == 0.0 && p.C[7] == 0.0 ? 2 : 1;
 }
 
+// The bin steps bin_xkey needs, as the search's arguments hold them.
+XKey xkey_of(const Plan& p)
+{
+    XKey k;
+    k.hbx = (float)(p.C[3] / p.nb[1]);
+    k.hcx = (float)(p.C[6] / p.nb[2]);
+    k.hcy = (float)(p.C[7] / p.nb[2]);
+    k.inv_hby = (float)(p.nb[1] / p.C[4]);
+    k.inv_hcz = (float)(p.nb[2] / p.C[8]);
+    return k;
+}
+
 GridArgs grid_args(const Plan& p)
 {
     GridArgs g;
@@ -2297,7 +2346,8 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
         o.inv = p.subset ? at<int>(ws, p.o_inv) : (int*)nullptr;
         o.stmp = at<void>(ws, p.o_stmp);
         o.xflag = totals + 4;
-        o.xorder = cell_shape(p) == 2;  // (only the orthorhombic count cuts bins by x)
+        o.xorder = cell_shape(p) != 0;  // (the count cuts bins by x in lower-triangular cells)
+        o.xk = xkey_of(p);
         if (narrow)
             hipLaunchKernelGGL((tile_sort_kernel<false, uint32_t>), dim3((unsigned)p.ntiles), dim3(256), 0, s, p.n,
                                p.tb, p.ntiles, (const int*)tstart, at<uint32_t>(ws, p.o_arr), bstart, o);
@@ -2391,9 +2441,11 @@ void launch_sort(const Plan& p, const void* pos, const int64_t* target_idx, void
 void launch_count_kernel(const SearchArgs& a, unsigned grid, hipStream_t s)
 {
     if (a.lowtri == 2 && a.xsplit)
-        hipLaunchKernelGGL((search_kernel<0, true>), dim3(grid), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((search_kernel<0, 1>), dim3(grid), dim3(kBlock), 0, s, a);
+    else if (a.lowtri == 1 && a.xsplit)
+        hipLaunchKernelGGL((search_kernel<0, 2>), dim3(grid), dim3(kBlock), 0, s, a);
     else
-        hipLaunchKernelGGL((search_kernel<0, false>), dim3(grid), dim3(kBlock), 0, s, a);
+        hipLaunchKernelGGL((search_kernel<0, 0>), dim3(grid), dim3(kBlock), 0, s, a);
 }
 #endif  // DG_MAIN_TU
 

@@ -3,7 +3,8 @@ a tile bucket of more than 2048 entries (tile-level sort), a bin of more than 12
 targets (per-bin sort, used above 36000 tiles).  Those segments are sorted in global memory
 (dg_segsort.hpp), so the order of the output is a function of the input alone: atoms in a bin
 by id, explicit targets in a bin by their position in the caller's list.  (Bins sorted in LDS
-order atoms of an orthorhombic cell by their x offset in the bin first, then by id.)
+order the atoms of a lower-triangular cell by their offset along the a axis in the bin
+first, then by id.)
 
 Each case puts a clump of atoms, scattered over the atom ids, inside one bin of a uniform
 box.  The clump's atoms then share one bin, so their first appearances as targets in
