@@ -533,8 +533,9 @@ __global__ __launch_bounds__(256) void tile_sort_kernel(int64_t n, int tb, int64
     uint32_t qx[kTileSortPer];
 #pragma unroll
     for (int u = 0; u < kTileSortPer; ++u) {
-        if constexpr (TGT) qx[u] = 0;
-        else qx[u] = o.xorder ? float_order_key(bin_xkey(q[u], o.xk)) : 0u;
+        qx[u] = 0;
+        if constexpr (!TGT)
+            if (qi[u] >= 0 && o.xorder) qx[u] = float_order_key(bin_xkey(q[u], o.xk));
         if (qi[u] >= 0) {
             const int d = atomicAdd(&S.cnt[ql[u]], 1);
             S.by[d] = qi[u];
