@@ -1555,6 +1555,10 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         int found2 = 0;  // twice the neighbours found so far
         // candidate range [va, vb) of row ri (oz * nry + oy) of this lane, chunk-local;
         // empty when the padded cutoff sphere misses the row
+        // (QS 1: rprune2 - gz^2 of the layer oz = gz_oz, kept while the rows of one z
+        // layer go by; gz_oz is uniform)
+        float gzz = 0.f;
+        int gz_oz = -1;
         auto row_range = [&](int ri, int c0, int c1, int& va, int& vb) {
             const int oz = ri / nry, oy = ri - oz * nry;
             int xlo = 0, xhi = nrx - 1;
@@ -1564,10 +1568,22 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
                 // orthorhombic: the row's bins span y in [py, py + 1] hby and z in
                 // [pz, pz + 1] hcz around the target; their gaps (less the margin) bound the
                 // distance from below, and the x range follows without shear
-                const float py = (float)(oy - a.P[1]) - Oy, pz = (float)(oz - a.P[2]) - Oz;
+                const float py = (float)(oy - a.P[1]) - Oy;
                 const float gy = fmaxf(fmaxf(fmaf(py, a.hby, -a.pmargin), fmaf(-py, a.hby, a.gy_off)), 0.f);
-                const float gz = fmaxf(fmaxf(fmaf(pz, a.hcz, -a.pmargin), fmaf(-pz, a.hcz, a.gz_off)), 0.f);
-                const float rem2 = fmaf(-gz, gz, fmaf(-gy, gy, a.rprune2));
+                float rem2;
+                if constexpr (QS == 1) {
+                    if (oz != gz_oz) {
+                        const float pz = (float)(oz - a.P[2]) - Oz;
+                        const float gz = fmaxf(fmaxf(fmaf(pz, a.hcz, -a.pmargin), fmaf(-pz, a.hcz, a.gz_off)), 0.f);
+                        gzz = fmaf(-gz, gz, a.rprune2);
+                        gz_oz = oz;
+                    }
+                    rem2 = fmaf(-gy, gy, gzz);
+                } else {
+                    const float pz = (float)(oz - a.P[2]) - Oz;
+                    const float gz = fmaxf(fmaxf(fmaf(pz, a.hcz, -a.pmargin), fmaf(-pz, a.hcz, a.gz_off)), 0.f);
+                    rem2 = fmaf(-gz, gz, fmaf(-gy, gy, a.rprune2));
+                }
                 if (rem2 < 0.f) return;
                 const float rem = __builtin_amdgcn_sqrtf(rem2);
                 if constexpr (QS == 1) {
