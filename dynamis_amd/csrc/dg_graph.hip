@@ -307,8 +307,8 @@ __global__ void order_atoms_kernel(int64_t n, const uint32_t* __restrict__ key,
 // per-bin counting sort): kSortChunks workgroups each histogram the tiles of one chunk of
 // atoms in LDS and reserve their share of every tile with one device atomic per tile;
 // the same chunks then place their atoms into tile buckets; one workgroup per tile then
-// orders its bucket by (bin, x in the bin, atom id) in LDS and writes the bin starts and the
-// cell list.
+// orders its bucket by (bin, offset along the a axis in the bin for lower-triangular cells,
+// atom id) in LDS and writes the bin starts and the cell list.
 
 // Chunk c of the atoms: [c n / G, (c + 1) n / G).
 __device__ __forceinline__ void sort_chunk(int64_t n, int64_t* lo, int64_t* hi)
