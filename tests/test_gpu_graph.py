@@ -524,6 +524,29 @@ def test_near_cutoff_pairs_along_x(cuda, dtype, shape):
     assert len(o["src"]) > 0.1 * vol * 30
 
 
+@pytest.mark.parametrize("shape", ["cubic", "lowtri"])
+def test_crowded_bins_in_sparse_rows(cuda, shape):
+    """Bins of 16 to 80 atoms (spread over the whole bin) in a background at C3's density,
+    each tile still one LDS chunk: the count's quarter-bin prefix counts saturate at 15 in
+    these bins, and rows that start or end in them must fall back to the whole bin on the
+    saturated side."""
+    cell = {"cubic": np.eye(3) * 45.0,
+            "lowtri": np.array([[45.0, 0, 0], [10.0, 44.0, 0], [-6.0, 8.0, 43.0]])}[shape]
+    r = 6.0
+    rng = np.random.default_rng(37)
+    vol = abs(np.linalg.det(cell))
+    bg = rng.uniform(0, 1, (int(0.1 * vol), 3))
+    nb = {"cubic": 15, "lowtri": 14}[shape]  # bins per axis: the planner's floor(2 d_face / r)
+    crowds = []
+    for k, m in enumerate([16, 24, 40, 80]):
+        b = rng.integers(0, nb, 3)
+        crowds.append((b + rng.uniform(0.0, 1.0, (m, 3))) / nb)  # inside one bin, in fractions
+    frac = np.concatenate([bg] + crowds)
+    pos = (frac @ cell).astype(np.float32)
+    _, _, cnt, o = check_parity(pos, cell, (1, 1, 1), r, cuda, name=f"crowded bins {shape}")
+    assert len(o["src"]) > 0
+
+
 @pytest.mark.parametrize("dtype", [np.float32, np.float64])
 @pytest.mark.parametrize("shape", ["cubic", "general"])
 def test_near_coincident_atoms(cuda, dtype, shape):
