@@ -1553,12 +1553,12 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
         // lane has finished its row r, and a lane that finishes early goes on into its row
         // r + 1 meanwhile, so a wave waits for its longest row less often.
         int found2 = 0;  // twice the neighbours found so far
-        // candidate range [va, vb) of row ri (oz * nry + oy) of this lane, chunk-local;
-        // empty when the padded cutoff sphere misses the row
         // (QS 1: rprune2 - gz^2 of the layer oz = gz_oz, kept while the rows of one z
         // layer go by; gz_oz is uniform)
         float gzz = 0.f;
         int gz_oz = -1;
+        // candidate range [va, vb) of row ri (oz * nry + oy) of this lane, chunk-local;
+        // empty when the padded cutoff sphere misses the row
         auto row_range = [&](int ri, int c0, int c1, int& va, int& vb) {
             const int oz = ri / nry, oy = ri - oz * nry;
             int xlo = 0, xhi = nrx - 1;
