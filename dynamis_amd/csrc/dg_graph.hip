@@ -1425,6 +1425,7 @@ __device__ __forceinline__ TileOut search_tile(const SearchArgs& a,
     // Entries cut off this way lie beyond the padded cutoff along x alone, so they are never
     // edges: every target's edge sequence is unchanged (the fix-up pass, which sweeps whole
     // bins, numbers edges alike).
+    static_assert(kCap < (1 << 20), "a one-chunk region's first entries fit the rp word's 20 bits");
     const bool qsplit = QS != 0 && nchunks == 1 && a.totals[4] == 0;
     XKey xkey;
     xkey.hbx = a.hbx; xkey.hcx = a.hcx; xkey.hcy = a.hcy; xkey.inv_hby = a.inv_hby; xkey.inv_hcz = a.inv_hcz;
