@@ -71,7 +71,8 @@ def main():
         return
     if args.gpus != 1:
         print(f"bench.py: this build measures one GPU only (asked for --gpus {args.gpus}); the "
-              "graph build shards by space with no collective inside it -- see DESIGN.md.",
+              "graph build shards by space (each rank builds its own atoms' graph with a ghost shell), with no "
+              "collective inside it.",
               file=sys.stderr)
         sys.exit(2)
 
